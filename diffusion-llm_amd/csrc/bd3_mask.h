@@ -1,0 +1,197 @@
+// bd3_mask.h - integer-only BD3-LM mask predicates and tile classification,
+// shared by the gfx950 kernels and the host (C-ABI census helpers, CPU tests).
+//
+// Training layout: the attention sequence is cat(x_t, x_0) of length 2n.
+// Index < n is the noisy copy x_t, index >= n the clean copy x_0; the block id
+// of an index is (index mod n) / bs. Rules (model/bd3lm.py:17-21, :41-52):
+//   noisy row, block b -> noisy keys of block b          (block diagonal)
+//   noisy row, block b -> clean keys of blocks < b       (offset block-causal)
+//   clean row, block b -> clean keys of blocks <= b      (block-causal)
+//   clean row          -> noisy keys: never
+// The same predicate is stated by the FlexAttention mask_mod
+// (bench/attention_bench.py:25-38) and the Triton bd3lm_mask
+// (kernels/BlockSparseFlashAttention.py:12-30).
+//
+// Decode layout: queries are the last q_len of kv_len positions; row i sits
+// at position p = kv_len - q_len + i and sees key j iff j / bs <= p / bs and
+// j < kv_len (kernels/BlockSparseDecodeAttention.py:84-88, :23-26), i.e. the
+// clean-clean quadrant of the training mask sliced as model/bd3lm.py:168.
+#pragma once
+
+#include <stdint.h>
+
+#if defined(__HIPCC__) || defined(__HIP__)
+#define BD3_HD __host__ __device__ __forceinline__
+#else
+#define BD3_HD static inline
+#endif
+
+namespace bd3 {
+
+BD3_HD int imin(int a, int b) { return a < b ? a : b; }
+BD3_HD int imax(int a, int b) { return a > b ? a : b; }
+
+// Training mask: may row q attend to key k (both in [0, 2n))?
+BD3_HD bool train_visible(int q, int k, int n, int bs) {
+  const bool qc = q >= n, kc = k >= n;
+  const int qb = (qc ? q - n : q) / bs;
+  const int kb = (kc ? k - n : k) / bs;
+  if (!qc && !kc) return qb == kb;
+  if (!qc && kc) return kb < qb;
+  if (qc && kc) return kb <= qb;
+  return false;
+}
+
+// Decode mask: may query row i (of q_len, the last positions) attend to key j?
+BD3_HD bool decode_visible(int i, int j, int q_len, int kv_len, int bs) {
+  const int p = kv_len - q_len + i;
+  return j < kv_len && (j / bs) <= (p / bs);
+}
+
+// Visible-key count of one training row (its live pairs), for the census.
+// Noisy row of block b: its own block [bs*b, min(bs*(b+1), n)) plus the bs*b
+// earlier clean keys; clean row of block b: min(bs*(b+1), n) clean keys.
+BD3_HD int train_row_keys(int q, int n, int bs) {
+  const int b = (q < n ? q : q - n) / bs;
+  return imin(bs * (b + 1), n);
+}
+
+// The keys one training row sees, as two half-open intervals of global key
+// indices: key k is visible iff lo1 <= k < hi1 or lo2 <= k < hi2. Equivalent
+// to train_visible(q, k, n, bs) for every k in [0, 2n).
+struct RowIntervals {
+  int lo1, hi1, lo2, hi2;
+};
+
+BD3_HD RowIntervals train_row_intervals(int q, int n, int bs) {
+  RowIntervals r;
+  if (q < n) {
+    const int b = q / bs;
+    r.lo1 = bs * b;
+    r.hi1 = imin(bs * (b + 1), n);
+    r.lo2 = n;
+    r.hi2 = n + bs * b;
+  } else {
+    const int b = (q - n) / bs;
+    r.lo1 = n;
+    r.hi1 = n + imin(bs * (b + 1), n);
+    r.lo2 = 0;
+    r.hi2 = 0;
+  }
+  return r;
+}
+
+BD3_HD bool row_sees(const RowIntervals& r, int k) {
+  return (k >= r.lo1 && k < r.hi1) || (k >= r.lo2 && k < r.hi2);
+}
+
+enum TileClass { kNone = 0, kFull = 1, kPartial = 2 };
+
+// Classification of the pairs (rows [q0, q0+R), keys [k0, k0+C)) under the
+// training mask. Rows must lie in one half and keys in one half (true for
+// 32-aligned groups when n % 32 == 0). kNone and kFull are exact; kPartial
+// means some but not all pairs are live.
+BD3_HD int train_class(int q0, int R, int k0, int C, int n, int bs) {
+  const bool qc = q0 >= n, kc = k0 >= n;
+  const int r0 = qc ? q0 - n : q0;
+  const int r1 = r0 + R - 1;
+  const int b0 = r0 / bs, b1 = r1 / bs;
+  const int a = kc ? k0 - n : k0;  // key offset inside its half
+  const int e = a + C;
+  if (!qc && !kc) {  // block diagonal
+    const int lo = bs * b0, hi = imin(bs * (b1 + 1), n);
+    if (e <= lo || a >= hi) return kNone;
+    if (b0 == b1 && lo <= a && e <= hi) return kFull;
+    return kPartial;
+  }
+  if (!qc && kc) {  // row in block b sees clean keys [0, bs*b)
+    if (a >= bs * b1) return kNone;
+    if (e <= bs * b0) return kFull;
+    return kPartial;
+  }
+  if (qc && kc) {  // row in block b sees clean keys [0, min(bs*(b+1), n))
+    if (a >= imin(bs * (b1 + 1), n)) return kNone;
+    if (e <= imin(bs * (b0 + 1), n)) return kFull;
+    return kPartial;
+  }
+  return kNone;  // clean rows never see noisy keys
+}
+
+// Key ranges (in key-tile units of `tile` keys) a training row group
+// [q0, q0+R) must visit: up to two half-open tile ranges [t0, t1) and
+// [t2, t3). Rows must lie in one half. Every live pair of the group lies in
+// the union of the ranges (tiles may still hold dead pairs).
+struct KeyRanges {
+  int t0, t1, t2, t3;
+};
+
+BD3_HD KeyRanges train_key_ranges(int q0, int R, int n, int bs, int tile) {
+  KeyRanges r;
+  const bool qc = q0 >= n;
+  const int r0 = qc ? q0 - n : q0;
+  const int r1 = r0 + R - 1;
+  const int b0 = r0 / bs, b1 = r1 / bs;
+  if (!qc) {
+    // own noisy blocks, then earlier clean blocks
+    r.t0 = (bs * b0) / tile;
+    r.t1 = (imin(bs * (b1 + 1), n) + tile - 1) / tile;
+    r.t2 = n / tile;
+    r.t3 = (n + bs * b1 + tile - 1) / tile;
+  } else {
+    r.t0 = n / tile;
+    r.t1 = (n + imin(bs * (b1 + 1), n) + tile - 1) / tile;
+    r.t2 = 0;
+    r.t3 = 0;
+  }
+  return r;
+}
+
+// Query ranges (in query-tile units) that see a training key group
+// [k0, k0+C) (keys in one half), the transpose of train_key_ranges: up to two
+// half-open tile ranges. Used by the backward (one program per key tile).
+BD3_HD KeyRanges train_query_ranges(int k0, int C, int n, int bs, int tile) {
+  KeyRanges r;
+  const bool kc = k0 >= n;
+  const int a0 = kc ? k0 - n : k0;
+  const int a1 = a0 + C - 1;
+  const int kb0 = a0 / bs, kb1 = a1 / bs;
+  if (!kc) {
+    // noisy keys: noisy rows of the same blocks
+    r.t0 = (bs * kb0) / tile;
+    r.t1 = (imin(bs * (kb1 + 1), n) + tile - 1) / tile;
+    r.t2 = 0;
+    r.t3 = 0;
+  } else {
+    // clean keys of block kb: noisy rows of blocks > kb, clean rows of
+    // blocks >= kb
+    const int noisy_lo = imin(bs * (kb0 + 1), n);
+    r.t0 = noisy_lo / tile;
+    r.t1 = n / tile;
+    if (r.t0 >= r.t1) { r.t0 = 0; r.t1 = 0; }
+    r.t2 = (n + bs * kb0) / tile;
+    r.t3 = (2 * n) / tile;
+  }
+  return r;
+}
+
+// Decode: classification of rows [i0, i0+R) (R >= 1, clamp to q_len done by
+// the caller) against keys [j0, j0+C).
+BD3_HD int decode_class(int i0, int R, int j0, int C, int q_len, int kv_len,
+                        int bs) {
+  const int i1 = imin(i0 + R, q_len) - 1;
+  const int p0 = kv_len - q_len + i0, p1 = kv_len - q_len + i1;
+  const int hi_first = imin((p0 / bs + 1) * bs, kv_len);  // row i0 sees [0, hi_first)
+  const int hi_last = imin((p1 / bs + 1) * bs, kv_len);
+  if (j0 >= hi_last) return kNone;
+  if (j0 + C <= hi_first && i0 + R <= q_len) return kFull;
+  return kPartial;
+}
+
+// Decode: one past the last key any row in [i0, i0+R) may see.
+BD3_HD int decode_key_end(int i0, int R, int q_len, int kv_len, int bs) {
+  const int i1 = imin(i0 + R, q_len) - 1;
+  const int p1 = kv_len - q_len + i1;
+  return imin((p1 / bs + 1) * bs, kv_len);
+}
+
+}  // namespace bd3

@@ -1,0 +1,318 @@
+// capi.hip - the extern "C" boundary of libbd3attn.so (declared in
+// include/bd3attn.h): argument validation, workspace sizing, launches and
+// host-only census helpers. Validation failures return BD3_EINVAL before any
+// HIP call, so they are testable on a machine without a GPU.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "bd3_launch.h"
+#include "bd3_mask.h"
+#include "bd3attn.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return BD3_OK;
+  return fail(BD3_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Rows of 64 bf16 are read as 16-byte vectors: the base must be 16-byte
+// aligned and every outer stride a multiple of 8 elements.
+int check_tensor(const void* p, const int64_t* st, const char* name) {
+  if (p == nullptr) return fail(BD3_EINVAL, "%s is NULL", name);
+  if (!aligned16(p)) return fail(BD3_EINVAL, "%s must be 16-byte aligned", name);
+  for (int i = 0; i < 3; ++i)
+    if (st[i] % 8 != 0 || st[i] < 0)
+      return fail(BD3_EINVAL, "%s stride[%d]=%lld must be a non-negative multiple of 8", name, i,
+                  (long long)st[i]);
+  return BD3_OK;
+}
+
+bd3::Strides3 s3(const int64_t* st) { return bd3::Strides3{st[0], st[1], st[2]}; }
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+constexpr int kDecodeQT = 32;
+
+int decode_q_tiles(int q_len) { return (q_len + kDecodeQT - 1) / kDecodeQT; }
+
+int check_common_decode(const void* q, const void* k, const void* v, void* o, int batch,
+                        int heads, int q_len, int kv_len, int head_dim, int block_size,
+                        const int64_t* strides) {
+  if (batch < 1 || heads < 1) return fail(BD3_EINVAL, "batch and heads must be >= 1");
+  if (head_dim != bd3::kHeadDim) return fail(BD3_EINVAL, "head_dim must be 64, got %d", head_dim);
+  if (block_size < 1) return fail(BD3_EINVAL, "block_size must be >= 1");
+  if (q_len < 1 || q_len > kv_len)
+    return fail(BD3_EINVAL, "queries are the last q_len key positions: need 1 <= q_len (%d) <= kv_len (%d)",
+                q_len, kv_len);
+  if (strides == nullptr) return fail(BD3_EINVAL, "strides is NULL");
+  const char* names[4] = {"q", "k", "v", "o"};
+  const void* ptrs[4] = {q, k, v, o};
+  for (int i = 0; i < 4; ++i) {
+    int st = check_tensor(ptrs[i], strides + 3 * i, names[i]);
+    if (st) return st;
+  }
+  return BD3_OK;
+}
+
+int32_t auto_splits(int32_t batch, int32_t heads, int32_t q_len, int32_t kv_len) {
+  // Aim for about four workgroups per CU on a 256-CU part, never fewer than
+  // 128 keys per split, and never more than the reference's rule would use.
+  const int64_t base = (int64_t)batch * heads * decode_q_tiles(q_len);
+  const int64_t target = 1024;
+  int64_t s = (target + base - 1) / base;
+  const int64_t max_by_len = kv_len / 128 > 0 ? kv_len / 128 : 1;
+  if (s > max_by_len) s = max_by_len;
+  if (s < 1) s = 1;
+  return (int32_t)s;
+}
+
+int run_decode(const void* q, const void* k, const void* v, void* o, int32_t batch,
+               int32_t heads, int32_t q_len, int32_t kv_len, int32_t block_size,
+               int32_t n_splits, const int64_t* strides, float scale, void* workspace,
+               size_t workspace_bytes, void* stream) {
+  const int q_tiles = decode_q_tiles(q_len);
+  const size_t need = bd3_decode_workspace_bytes(batch, heads, q_len, kv_len, bd3::kHeadDim, n_splits);
+  if (workspace_bytes < need)
+    return fail(BD3_EINVAL, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
+  if (need > 0 && (workspace == nullptr || !aligned16(workspace)))
+    return fail(BD3_EINVAL, "workspace must be a 16-byte aligned device pointer");
+  bd3::DecodeArgs a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.o = static_cast<uint16_t*>(o);
+  const size_t po_bytes = (size_t)batch * heads * q_tiles * n_splits * kDecodeQT * bd3::kHeadDim * 4;
+  a.part_o = n_splits > 1 ? static_cast<float*>(workspace) : nullptr;
+  a.part_lse = n_splits > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + align256(po_bytes))
+                            : nullptr;
+  a.sq = s3(strides);
+  a.sk = s3(strides + 3);
+  a.sv = s3(strides + 6);
+  a.so = s3(strides + 9);
+  a.heads = heads;
+  a.bh = batch * heads;
+  a.q_len = q_len;
+  a.kv_len = kv_len;
+  a.bs = block_size;
+  a.n_splits = n_splits;
+  // Split length: ceil(kv_len / n_splits) rounded up to 16 keys.
+  int sl = (kv_len + n_splits - 1) / n_splits;
+  sl = (sl + 15) / 16 * 16;
+  a.split_len = sl;
+  a.q_tiles = q_tiles;
+  a.scale_log2 = scale * bd3::kLog2e;
+  return hip_status(bd3::launch_decode(a, kDecodeQT, static_cast<hipStream_t>(stream)), "decode launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+int bd3_abi_version(void) { return BD3_ABI_VERSION; }
+
+const char* bd3_last_error(void) { return g_err.c_str(); }
+
+int bd3_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int32_t batch,
+                 int32_t heads, int32_t n, int32_t head_dim, int32_t block_size,
+                 const int64_t* strides, float scale, void* stream) {
+  if (batch < 1 || heads < 1) return fail(BD3_EINVAL, "batch and heads must be >= 1");
+  if (head_dim != bd3::kHeadDim) return fail(BD3_EINVAL, "head_dim must be 64, got %d", head_dim);
+  if (n < 128 || n % 128 != 0)
+    return fail(BD3_EINVAL, "n (half the sequence) must be a positive multiple of 128, got %d", n);
+  if (block_size < 1) return fail(BD3_EINVAL, "block_size must be >= 1");
+  if (strides == nullptr) return fail(BD3_EINVAL, "strides is NULL");
+  const char* names[4] = {"q", "k", "v", "o"};
+  const void* ptrs[4] = {q, k, v, o};
+  for (int i = 0; i < 4; ++i) {
+    int st = check_tensor(ptrs[i], strides + 3 * i, names[i]);
+    if (st) return st;
+  }
+  if (lse == nullptr) return fail(BD3_EINVAL, "lse is NULL");
+  bd3::FwdArgs a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.o = static_cast<uint16_t*>(o);
+  a.lse = lse;
+  a.sq = s3(strides);
+  a.sk = s3(strides + 3);
+  a.sv = s3(strides + 6);
+  a.so = s3(strides + 9);
+  a.heads = heads;
+  a.bh = batch * heads;
+  a.n = n;
+  a.bs = block_size;
+  a.scale_log2 = scale * bd3::kLog2e;
+  return hip_status(bd3::launch_attn_fwd(a, static_cast<hipStream_t>(stream)), "attn_fwd launch");
+}
+
+size_t bd3_attn_bwd_workspace_bytes(int32_t batch, int32_t heads, int32_t n, int32_t head_dim) {
+  if (batch < 1 || heads < 1 || n < 1 || head_dim < 1) return 0;
+  const size_t rows = (size_t)batch * heads * 2 * n;
+  return align256(rows * sizeof(float)) + align256(rows * head_dim * sizeof(float));
+}
+
+int bd3_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                 const float* lse, void* dq, void* dk, void* dv, void* workspace,
+                 size_t workspace_bytes, int32_t batch, int32_t heads, int32_t n,
+                 int32_t head_dim, int32_t block_size, const int64_t* strides, float scale,
+                 void* stream) {
+  if (batch < 1 || heads < 1) return fail(BD3_EINVAL, "batch and heads must be >= 1");
+  if (head_dim != bd3::kHeadDim) return fail(BD3_EINVAL, "head_dim must be 64, got %d", head_dim);
+  if (n < 128 || n % 128 != 0)
+    return fail(BD3_EINVAL, "n (half the sequence) must be a positive multiple of 128, got %d", n);
+  if (block_size < 1 || n % block_size != 0)
+    return fail(BD3_EINVAL, "n (%d) must be a multiple of block_size (%d)", n, block_size);
+  if (strides == nullptr) return fail(BD3_EINVAL, "strides is NULL");
+  const char* names[8] = {"q", "k", "v", "o", "dout", "dq", "dk", "dv"};
+  const void* ptrs[8] = {q, k, v, o, dout, dq, dk, dv};
+  for (int i = 0; i < 8; ++i) {
+    int st = check_tensor(ptrs[i], strides + 3 * i, names[i]);
+    if (st) return st;
+  }
+  if (lse == nullptr) return fail(BD3_EINVAL, "lse is NULL");
+  const size_t need = bd3_attn_bwd_workspace_bytes(batch, heads, n, head_dim);
+  if (workspace == nullptr || !aligned16(workspace) || workspace_bytes < need)
+    return fail(BD3_EINVAL, "workspace must be a 16-byte aligned buffer of >= %zu bytes", need);
+  const size_t rows = (size_t)batch * heads * 2 * n;
+  bd3::BwdArgs a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.o = static_cast<const uint16_t*>(o);
+  a.dout = static_cast<const uint16_t*>(dout);
+  a.lse = lse;
+  a.dq = static_cast<uint16_t*>(dq);
+  a.dk = static_cast<uint16_t*>(dk);
+  a.dv = static_cast<uint16_t*>(dv);
+  a.delta = static_cast<float*>(workspace);
+  a.dq_acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + align256(rows * sizeof(float)));
+  a.sq = s3(strides);
+  a.sk = s3(strides + 3);
+  a.sv = s3(strides + 6);
+  a.so = s3(strides + 9);
+  a.sdo = s3(strides + 12);
+  a.sdq = s3(strides + 15);
+  a.sdk = s3(strides + 18);
+  a.sdv = s3(strides + 21);
+  a.heads = heads;
+  a.bh = batch * heads;
+  a.n = n;
+  a.bs = block_size;
+  a.scale = scale;
+  a.scale_log2 = scale * bd3::kLog2e;
+  return hip_status(bd3::launch_attn_bwd(a, static_cast<hipStream_t>(stream)), "attn_bwd launch");
+}
+
+int32_t bd3_decode_auto_splits(int32_t batch, int32_t heads, int32_t q_len, int32_t kv_len) {
+  if (batch < 1 || heads < 1 || q_len < 1 || kv_len < 1) return 1;
+  return auto_splits(batch, heads, q_len, kv_len);
+}
+
+size_t bd3_decode_workspace_bytes(int32_t batch, int32_t heads, int32_t q_len, int32_t kv_len,
+                                  int32_t head_dim, int32_t n_splits) {
+  if (batch < 1 || heads < 1 || q_len < 1 || kv_len < 1) return 0;
+  if (n_splits == 0) n_splits = auto_splits(batch, heads, q_len, kv_len);
+  if (n_splits <= 1) return 0;
+  const size_t slots = (size_t)batch * heads * decode_q_tiles(q_len) * n_splits * kDecodeQT;
+  return align256(slots * head_dim * sizeof(float)) + align256(slots * sizeof(float));
+}
+
+int bd3_decode(const void* q, const void* k, const void* v, void* o, int32_t batch, int32_t heads,
+               int32_t q_len, int32_t kv_len, int32_t head_dim, int32_t block_size,
+               const int64_t* strides, float scale, void* workspace, size_t workspace_bytes,
+               void* stream) {
+  int st = check_common_decode(q, k, v, o, batch, heads, q_len, kv_len, head_dim, block_size, strides);
+  if (st) return st;
+  const int32_t ns = auto_splits(batch, heads, q_len, kv_len);
+  return run_decode(q, k, v, o, batch, heads, q_len, kv_len, block_size, ns, strides, scale,
+                    workspace, workspace_bytes, stream);
+}
+
+int bd3_decode_splitkv(const void* q, const void* k, const void* v, void* o, int32_t batch,
+                       int32_t heads, int32_t q_len, int32_t kv_len, int32_t head_dim,
+                       int32_t block_size, int32_t n_splits, const int64_t* strides, float scale,
+                       void* workspace, size_t workspace_bytes, void* stream) {
+  int st = check_common_decode(q, k, v, o, batch, heads, q_len, kv_len, head_dim, block_size, strides);
+  if (st) return st;
+  if (n_splits == 0) n_splits = (kv_len + 255) / 256;  // reference SPLIT_N = 256 rule
+  if (n_splits < 1 || n_splits > kv_len)
+    return fail(BD3_EINVAL, "n_splits must be in [1, kv_len], got %d", n_splits);
+  return run_decode(q, k, v, o, batch, heads, q_len, kv_len, block_size, n_splits, strides, scale,
+                    workspace, workspace_bytes, stream);
+}
+
+int bd3_mask_dump(uint8_t* out, int32_t mode, int32_t rows, int32_t kv_len, int32_t block_size,
+                  void* stream) {
+  if (out == nullptr) return fail(BD3_EINVAL, "out is NULL");
+  if (block_size < 1) return fail(BD3_EINVAL, "block_size must be >= 1");
+  if (mode == 0) {
+    if (rows < 1) return fail(BD3_EINVAL, "n must be >= 1");
+  } else if (mode == 1) {
+    if (rows < 1 || rows > kv_len) return fail(BD3_EINVAL, "need 1 <= q_len <= kv_len");
+  } else {
+    return fail(BD3_EINVAL, "mode must be 0 (training) or 1 (decode)");
+  }
+  return hip_status(bd3::launch_mask_dump(out, mode, rows, kv_len, block_size,
+                                          static_cast<hipStream_t>(stream)),
+                    "mask_dump launch");
+}
+
+int bd3_train_classify(int32_t n, int32_t block_size, int32_t q0, int32_t k0) {
+  if (n < 32 || n % 32 != 0 || block_size < 1) return -1;
+  if (q0 < 0 || k0 < 0 || q0 + 32 > 2 * n || k0 + 32 > 2 * n || q0 % 32 || k0 % 32) return -1;
+  return bd3::train_class(q0, 32, k0, 32, n, block_size);
+}
+
+int bd3_train_tile_census(int32_t n, int32_t block_size, int64_t* out) {
+  if (out == nullptr) return fail(BD3_EINVAL, "out is NULL");
+  if (n < 128 || n % 128 != 0 || block_size < 1)
+    return fail(BD3_EINVAL, "need n a positive multiple of 128 and block_size >= 1");
+  int64_t useful = 0, executed = 0, full = 0, partial = 0, skipped = 0;
+  for (int q = 0; q < 2 * n; ++q) useful += bd3::train_row_keys(q, n, block_size);
+  // The forward's schedule: 128-row workgroups visit the 64-key tiles of
+  // train_key_ranges; each 32-row wave classifies each 32-key sub-block.
+  for (int q0 = 0; q0 < 2 * n; q0 += 128) {
+    const bd3::KeyRanges kr = bd3::train_key_ranges(q0, 128, n, block_size, 64);
+    const int ranges[2][2] = {{kr.t0, kr.t1}, {kr.t2, kr.t3}};
+    for (int rg = 0; rg < 2; ++rg)
+      for (int t = ranges[rg][0]; t < ranges[rg][1]; ++t)
+        for (int w = 0; w < 4; ++w)
+          for (int sb = 0; sb < 2; ++sb) {
+            const int c = bd3::train_class(q0 + 32 * w, 32, 64 * t + 32 * sb, 32, n, block_size);
+            if (c == bd3::kNone) {
+              ++skipped;
+            } else {
+              executed += 32 * 32;
+              if (c == bd3::kFull) ++full; else ++partial;
+            }
+          }
+  }
+  const int64_t nn = n, bs = block_size;
+  out[0] = useful;
+  out[1] = executed;
+  out[2] = full;
+  out[3] = partial;
+  out[4] = skipped;
+  out[5] = nn * nn + nn * bs;
+  return BD3_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,191 @@
+/*
+ * bd3attn.h - C ABI of the MI355X (gfx950) BD3-LM attention library
+ * (libbd3attn.so).
+ *
+ * Scope: the attention hot path of block-diffusion language models.
+ *   - training attention forward/backward over cat(x_t, x_0) (length 2n)
+ *     under the BD3-LM block-diffusion mask;
+ *   - block-sparse decode attention of the last q_len positions over a
+ *     KV cache of kv_len positions (block-causal);
+ *   - split-KV decode attention (partials + LSE merge).
+ *
+ * Conventions shared by every entry point:
+ *   - All tensor pointers are DEVICE pointers to bf16 data (uint16 bit
+ *     patterns of bfloat16) unless the type says float. Row-major 4-D
+ *     tensors (batch, heads, seq, head_dim) with the last stride 1;
+ *     `strides` passes the other three element strides (batch, head, seq)
+ *     of each tensor, in the order the entry point lists.
+ *   - The library never allocates device memory and never synchronises.
+ *     Work is enqueued on `stream` (a hipStream_t; NULL = default stream).
+ *     Workspaces are caller-allocated; *_workspace_bytes() sizes them.
+ *   - Every entry point returns 0 on success, BD3_EINVAL when an argument
+ *     violates a precondition (nothing is launched), or BD3_EHIP when the
+ *     HIP runtime reports an error. bd3_last_error() returns a thread-local
+ *     message describing the last failure on the calling thread.
+ *   - head_dim must be 64 (the reference's only configuration: d_model
+ *     768 / 12 heads).
+ *
+ * Reentrant: no mutable global state besides the thread-local error
+ * message.
+ */
+#ifndef BD3ATTN_H
+#define BD3ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BD3_OK 0
+#define BD3_EINVAL 1
+#define BD3_EHIP 2
+
+#define BD3_ABI_VERSION 1
+
+/* Version of this ABI (BD3_ABI_VERSION). No reference counterpart. */
+int bd3_abi_version(void);
+
+/* Thread-local message for the last non-zero status on this thread. */
+const char* bd3_last_error(void);
+
+/*
+ * Training attention forward:
+ *   O = softmax(Q K^T * scale + M) V,  lse = logsumexp(Q K^T * scale + M)
+ * over the 2n-long sequence cat(x_t, x_0), M the BD3-LM block-diffusion
+ * mask (model/bd3lm.py:10-52). lse is natural-log, fp32, contiguous
+ * (batch, heads, 2n).
+ * strides: 12 int64 = (b, h, s) element strides of q, k, v, o.
+ * Preconditions: n % 128 == 0, block_size >= 1, head_dim == 64.
+ *
+ * Replaces the launch of block_sparse_attention_fwd_kern in
+ * BlockSparseFlashAttention.forward
+ * (kernels/BlockSparseFlashAttention.py:466-506, kernel :75-172).
+ */
+int bd3_attn_fwd(const void* q, const void* k, const void* v, void* o,
+                 float* lse, int32_t batch, int32_t heads, int32_t n,
+                 int32_t head_dim, int32_t block_size, const int64_t* strides,
+                 float scale, void* stream);
+
+/*
+ * Bytes of workspace bd3_attn_bwd needs: Delta = rowsum(dO * O) and an
+ * fp32 dQ accumulator, both (batch, heads, 2n[, head_dim]).
+ * No reference counterpart (the reference allocates with torch.empty).
+ */
+size_t bd3_attn_bwd_workspace_bytes(int32_t batch, int32_t heads, int32_t n,
+                                    int32_t head_dim);
+
+/*
+ * Training attention backward: dQ, dK, dV of the forward above, given
+ * dO and the forward's O and lse. Delta = rowsum(dO * O) is computed
+ * inside (fused preprocess).
+ * strides: 24 int64 = (b, h, s) element strides of
+ *          q, k, v, o, dout, dq, dk, dv.
+ * Preconditions: as the forward, plus n % block_size == 0 and
+ * workspace_bytes >= bd3_attn_bwd_workspace_bytes(...).
+ *
+ * Replaces the Delta torch op and the launches of
+ * block_sparse_attention_bwd_dq_kern and
+ * block_sparse_attention_dk_dv_bwd_kern in
+ * BlockSparseFlashAttention.backward
+ * (kernels/BlockSparseFlashAttention.py:508-562; kernels :212-328, :368-452).
+ */
+int bd3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
+                 const void* dout, const float* lse, void* dq, void* dk,
+                 void* dv, void* workspace, size_t workspace_bytes,
+                 int32_t batch, int32_t heads, int32_t n, int32_t head_dim,
+                 int32_t block_size, const int64_t* strides, float scale,
+                 void* stream);
+
+/*
+ * Block-sparse decode attention: queries are the LAST q_len of kv_len
+ * positions; row i (position p = kv_len - q_len + i) sees key j iff
+ * j / block_size <= p / block_size (block-causal), j < kv_len.
+ * n_splits = 0 lets the library choose a key split that fills the GPU
+ * (a workspace of bd3_decode_workspace_bytes(..., 0, ...) is then needed;
+ * pass NULL/0 when that size is 0).
+ * strides: 12 int64 = (b, h, s) element strides of q, k, v, o.
+ * Preconditions: 1 <= q_len <= kv_len, head_dim == 64, block_size >= 1.
+ *
+ * Replaces block_sparse_decode_kern and its launch in
+ * block_sparse_decode_attention
+ * (kernels/BlockSparseDecodeAttention.py:40-110, :118-148).
+ */
+int bd3_decode(const void* q, const void* k, const void* v, void* o,
+               int32_t batch, int32_t heads, int32_t q_len, int32_t kv_len,
+               int32_t head_dim, int32_t block_size, const int64_t* strides,
+               float scale, void* workspace, size_t workspace_bytes,
+               void* stream);
+
+/*
+ * Number of key splits bd3_decode / bd3_decode_splitkv use for
+ * n_splits == 0 (auto). No reference counterpart.
+ */
+int32_t bd3_decode_auto_splits(int32_t batch, int32_t heads, int32_t q_len,
+                               int32_t kv_len);
+
+/*
+ * Workspace bytes for a split-KV decode with n_splits splits (0 = auto):
+ * fp32 partial O and LSE per (batch*head, query tile, split). 0 when a
+ * single split needs no workspace. No reference counterpart (the
+ * reference allocates o_part / lse with torch.empty,
+ * kernels/SplitKVDecodeAttention.py:148-151).
+ */
+size_t bd3_decode_workspace_bytes(int32_t batch, int32_t heads, int32_t q_len,
+                                  int32_t kv_len, int32_t head_dim,
+                                  int32_t n_splits);
+
+/*
+ * Split-KV decode attention: the keys [0, kv_len) are cut into n_splits
+ * contiguous ranges, each producing a normalised fp32 partial O and its
+ * LSE, merged with LSE weights (FlashDecoding). Same result as bd3_decode.
+ * n_splits = 0 means the reference rule ceil(kv_len / 256).
+ * strides: 12 int64 = (b, h, s) element strides of q, k, v, o.
+ * Preconditions: 1 <= q_len <= kv_len, head_dim == 64,
+ * 1 <= n_splits <= kv_len, workspace large enough.
+ *
+ * Replaces split_kv_kern + split_kv_reduce_kern and their launches in
+ * split_kv_decode_attention (kernels/SplitKVDecodeAttention.py:16-171).
+ */
+int bd3_decode_splitkv(const void* q, const void* k, const void* v, void* o,
+                       int32_t batch, int32_t heads, int32_t q_len,
+                       int32_t kv_len, int32_t head_dim, int32_t block_size,
+                       int32_t n_splits, const int64_t* strides, float scale,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Writes the mask the device predicate applies, one byte per (row, key)
+ * (1 = may attend), row-major:
+ *   mode 0 (training): (2n, 2n) with n = rows, kv_len ignored;
+ *   mode 1 (decode):   (rows = q_len, kv_len).
+ * For bit-exact comparison against block_diff_mask (model/bd3lm.py:10-52)
+ * and the decode slice (kernels/BlockSparseDecodeAttention.py:84-88).
+ */
+int bd3_mask_dump(uint8_t* out, int32_t mode, int32_t rows, int32_t kv_len,
+                  int32_t block_size, void* stream);
+
+/*
+ * Host-only (no GPU needed): tile census of the training-attention
+ * schedule. Writes out[0..5] =
+ *   {useful pairs, executed pairs (32x32 sub-blocks the forward computes),
+ *    full sub-blocks, partial sub-blocks, skipped sub-blocks,
+ *    useful pairs per (b,h) closed form n^2 + n*bs}
+ * for one (batch, head). Mirrors the reference's tile-skipping ranges
+ * (kernels/BlockSparseFlashAttention.py:132-164) at the library's own
+ * sub-block granularity.
+ */
+int bd3_train_tile_census(int32_t n, int32_t block_size, int64_t* out);
+
+/*
+ * Host-only: classification the device code uses for a 32-row query group
+ * starting at q0 and a 32-key sub-block starting at k0 in training mode:
+ * 0 = no live pair, 1 = every pair live, 2 = partial. For CPU tests.
+ */
+int bd3_train_classify(int32_t n, int32_t block_size, int32_t q0, int32_t k0);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BD3ATTN_H */

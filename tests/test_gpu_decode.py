@@ -1,0 +1,83 @@
+"""Decode attention (families D1, D2) on the GPU against the fp32 oracle.
+
+Bar: bf16 outputs within 2e-2 max-abs of the eager oracle (decode mask =
+the block-causal slice of the training mask), split-count invariance.
+"""
+import pytest
+import torch
+
+from _gpu_util import max_abs, splitkv_capi
+from kernels.BlockSparseDecodeAttention import block_sparse_decode_attention
+from kernels.SplitKVDecodeAttention import split_kv_decode_attention
+from oracle.attention import bf16_round, decode_attention, seeded_normal
+
+OUT_TOL = 2e-2
+
+
+def decode_inputs(B, H, q_len, kv_len, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = bf16_round(torch.randn(B, H, q_len, 64, generator=g))
+    k = bf16_round(torch.randn(B, H, kv_len, 64, generator=g))
+    v = bf16_round(torch.randn(B, H, kv_len, 64, generator=g))
+    return q, k, v
+
+
+CASES = [(2, 3, 16, 300, 16), (1, 2, 16, 16, 16), (2, 2, 32, 2048, 32), (1, 2, 1, 37, 4),
+         (1, 1, 200, 200, 16), (1, 2, 100, 300, 7), (2, 2, 64, 4112, 16), (1, 1, 130, 515, 64)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,H,q_len,kv_len,bs", CASES)
+def test_decode_matches_oracle(cuda, B, H, q_len, kv_len, bs):
+    q, k, v = decode_inputs(B, H, q_len, kv_len, seed=q_len + kv_len)
+    o = block_sparse_decode_attention(*(t.to(cuda, torch.bfloat16) for t in (q, k, v)), bs)
+    ref = decode_attention(q, k, v, bs)
+    torch.cuda.synchronize()
+    assert max_abs(o, ref) <= OUT_TOL
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,H,q_len,kv_len,bs", CASES)
+@pytest.mark.parametrize("n_splits", [1, 2, 5, 16])
+def test_splitkv_matches_oracle(cuda, B, H, q_len, kv_len, bs, n_splits):
+    if n_splits > kv_len:
+        pytest.skip("more splits than keys")
+    q, k, v = decode_inputs(B, H, q_len, kv_len, seed=7 * q_len + kv_len)
+    o = splitkv_capi(*(t.to(cuda, torch.bfloat16) for t in (q, k, v)), bs, n_splits)
+    ref = decode_attention(q, k, v, bs)
+    torch.cuda.synchronize()
+    assert max_abs(o, ref) <= OUT_TOL
+
+
+@pytest.mark.gpu
+def test_config3_split_invariance(cuda):
+    """32 sequences x 12 heads, 16 queries over a
+    4096 + 16 cache; splits {1, 4, 8, 16} and the reference default rule
+    all match the oracle and each other."""
+    B, H, q_len, kv_len, bs = 32, 12, 16, 4112, 16
+    q, k, v = decode_inputs(B, H, q_len, kv_len, seed=0)
+    qd, kd, vd = (t.to(cuda, torch.bfloat16) for t in (q, k, v))
+    ref = decode_attention(q, k, v, bs)
+    outs = [splitkv_capi(qd, kd, vd, bs, s) for s in (1, 4, 8, 16)]
+    outs.append(split_kv_decode_attention(qd, kd, vd, bs))
+    outs.append(block_sparse_decode_attention(qd, kd, vd, bs))
+    torch.cuda.synchronize()
+    for o in outs:
+        assert max_abs(o, ref) <= OUT_TOL
+    for o in outs[1:]:
+        assert max_abs(o, outs[0]) <= 1e-2
+
+
+@pytest.mark.gpu
+def test_decode_strided_cache_view(cuda):
+    """K/V read in place from a larger preallocated cache (outer strides of a
+    (B, H, L_max, d) buffer) equal the contiguous result."""
+    B, H, q_len, kv_len, L_max, bs = 2, 3, 16, 500, 1024, 16
+    kc = torch.randn(B, H, L_max, 64, device=cuda, dtype=torch.bfloat16)
+    vc = torch.randn(B, H, L_max, 64, device=cuda, dtype=torch.bfloat16)
+    q = torch.randn(B, H, q_len, 64, device=cuda, dtype=torch.bfloat16)
+    o1 = block_sparse_decode_attention(q, kc[:, :, :kv_len], vc[:, :, :kv_len], bs)
+    o2 = block_sparse_decode_attention(q, kc[:, :, :kv_len].contiguous(),
+                                       vc[:, :, :kv_len].contiguous(), bs)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)

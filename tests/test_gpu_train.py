@@ -1,0 +1,105 @@
+"""Training attention (family T) on the GPU against the fp32 eager oracle.
+
+Bar: bf16 outputs within 2e-2 max-abs of the fp32 oracle fed
+the same bf16-rounded inputs; gradients within 5e-2 relative Frobenius
+error; lse (natural log, what the forward saves) within 1e-2 abs.
+"""
+import pytest
+import torch
+
+from _gpu_util import bwd_capi, fwd_capi, max_abs, to_dev, train_inputs
+from kernels.BlockSparseFlashAttention import BlockSparseFlashAttention
+from oracle.attention import bd3_attention, bd3_attention_grads, rel_frobenius
+
+OUT_TOL = 2e-2
+GRAD_TOL = 5e-2
+LSE_TOL = 1e-2
+
+SMALL = [(1, 2, 128, 16), (2, 2, 256, 1), (2, 2, 256, 4), (1, 3, 256, 16), (2, 1, 256, 64),
+         (1, 2, 256, 256), (1, 2, 384, 32), (1, 1, 512, 16), (1, 2, 256, 3), (1, 1, 256, 100)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,H,n,bs", SMALL)
+def test_fwd_matches_oracle(cuda, B, H, n, bs):
+    q, k, v = train_inputs(B, H, n, seed=1, count=3)
+    o, lse = fwd_capi(*to_dev((q, k, v), cuda), bs)
+    ref_o, ref_lse = bd3_attention(q, k, v, bs)
+    torch.cuda.synchronize()
+    assert max_abs(o, ref_o) <= OUT_TOL
+    assert max_abs(lse, ref_lse) <= LSE_TOL
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,H,n,bs", [s for s in SMALL if s[2] % s[3] == 0])
+def test_bwd_matches_oracle(cuda, B, H, n, bs):
+    q, k, v, do = train_inputs(B, H, n, seed=2, count=4)
+    qd, kd, vd, dod = to_dev((q, k, v, do), cuda)
+    o, lse = fwd_capi(qd, kd, vd, bs)
+    dq, dk, dv = bwd_capi(qd, kd, vd, o, dod, lse, bs)
+    _, rdq, rdk, rdv = bd3_attention_grads(q, k, v, do, bs)
+    torch.cuda.synchronize()
+    for got, ref in ((dq, rdq), (dk, rdk), (dv, rdv)):
+        assert rel_frobenius(got.cpu(), ref) <= GRAD_TOL
+
+
+@pytest.mark.gpu
+def test_autograd_function_matches_capi(cuda):
+    """The reference-shaped autograd Function gives the C-ABI results."""
+    B, H, n, bs = 2, 2, 256, 16
+    q, k, v, do = to_dev(train_inputs(B, H, n, seed=3, count=4), cuda)
+    qg, kg, vg = (t.clone().requires_grad_(True) for t in (q, k, v))
+    o = BlockSparseFlashAttention.apply(qg, kg, vg, bs)
+    o.backward(do)
+    o2, lse = fwd_capi(q, k, v, bs)
+    dq, dk, dv = bwd_capi(q, k, v, o2, do, lse, bs)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o2)
+    for a, b in ((qg.grad, dq), (kg.grad, dk), (vg.grad, dv)):
+        assert max_abs(a, b) <= 1e-2  # fp32 atomics order may differ in dQ
+
+
+@pytest.mark.gpu
+def test_config0_plumbing(cuda):
+    """B=2, n=256, H=4, bs=16, q pre-scaled by 1/sqrt(d)."""
+    q, k, v = train_inputs(2, 4, 256, seed=0, count=3, q_scale=1 / 8)
+    o, _ = fwd_capi(*to_dev((q, k, v), cuda), 16)
+    ref_o, _ = bd3_attention(q, k, v, 16)
+    torch.cuda.synchronize()
+    assert max_abs(o, ref_o) <= OUT_TOL
+
+
+@pytest.mark.gpu
+def test_config1_full_size(cuda):
+    """BASELINE config 1 shape (B=8, L=1024, H=12, bs=16): forward and
+    backward against the oracle on a subset of (b, h) slices (each slice is
+    independent; the kernels run on the whole batch)."""
+    B, H, n, bs = 8, 12, 1024, 16
+    q, k, v, do = train_inputs(B, H, n, seed=0, count=4)
+    qd, kd, vd, dod = to_dev((q, k, v, do), cuda)
+    o, lse = fwd_capi(qd, kd, vd, bs)
+    dq, dk, dv = bwd_capi(qd, kd, vd, o, dod, lse, bs)
+    torch.cuda.synchronize()
+    for b, h in ((0, 0), (3, 7), (7, 11)):
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        ref_o, ref_lse = bd3_attention(q[sl], k[sl], v[sl], bs)
+        assert max_abs(o[sl], ref_o) <= OUT_TOL
+        assert max_abs(lse[sl], ref_lse) <= LSE_TOL
+        _, rdq, rdk, rdv = bd3_attention_grads(q[sl], k[sl], v[sl], do[sl], bs)
+        for got, ref in ((dq[sl], rdq), (dk[sl], rdk), (dv[sl], rdv)):
+            assert rel_frobenius(got.cpu(), ref) <= GRAD_TOL
+    assert torch.isfinite(o).all() and torch.isfinite(dq).all()
+    assert torch.isfinite(dk).all() and torch.isfinite(dv).all()
+
+
+@pytest.mark.gpu
+def test_strided_v_read_in_place(cuda):
+    """q, k, v as views of a fused (B, S, 3, H, d) projection (the model's QKV
+    split) give the same result as contiguous copies."""
+    B, H, n, bs = 1, 2, 128, 16
+    qkv = torch.randn(B, 2 * n, 3, H, 64, device=cuda, dtype=torch.bfloat16)
+    q, k, v = (qkv[:, :, i].permute(0, 2, 1, 3) for i in range(3))
+    o1, l1 = fwd_capi(q, k, v, bs)
+    o2, l2 = fwd_capi(q.contiguous(), k.contiguous(), v.contiguous(), bs)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)
