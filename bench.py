@@ -1,0 +1,336 @@
+#!/usr/bin/env python3
+"""Benchmark of the BD3-LM attention hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+Headline: one step = BD3-LM training attention
+forward + backward (bd3_attn_fwd then bd3_attn_bwd through the C ABI) at
+B=8, L=1024 (sequence 2048), H=12, d=64, block 16, bf16, q/k/v/dO ~ N(0,1)
+from seed 0, resident in HBM. value = useful fwd+bwd FLOPs per second:
+3.5 x 4*d*B*H*(n^2 + n*bs) (the reference's convention,
+bench/attention_bench.py:89,99, restricted to unmasked pairs).
+
+Printed on stdout as ONE JSON line, with:
+  roofline      the dominant kernel's useful TFLOP/s against bf16 dense MFMA
+                peak (events on the launch stream, averaged over the timed
+                steps);
+  cpu_baseline  the fp32 eager oracle's fwd+bwd on the host cores over a
+                bounded sample of (b, h) slices of the same workload;
+  decode        configs[3]: split-KV decode KV-read GB/s at splits
+                {1, 4, 8, 16}, the reference's default split rule and the
+                auto split, against 8 TB/s;
+  sweep         configs[2]: block sizes {4, 16, 64, 256} at B=4, L=2048,
+                H=16 (useful TFLOP/s and the schedule's useful fraction).
+Human-readable progress goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+for _p in (str(REPO), str(REPO / "diffusion-llm_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+D = 64
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def useful_fwd_flops(B, H, n, bs):
+    return 4 * D * B * H * (n * n + n * bs)
+
+
+def seeded_bf16(shape, seed, count, device):
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randn(shape, generator=g, dtype=torch.float32).to(device, torch.bfloat16)
+            for _ in range(count)]
+
+
+class TrainStep:
+    """Preallocated forward + backward of the training attention via the C ABI."""
+
+    def __init__(self, B, H, n, bs, device, seed=0):
+        import torch
+        from kernels._native import lib, ptr, stream_of, strides
+        self.B, self.H, self.n, self.bs = B, H, n, bs
+        self.q, self.k, self.v, self.do = seeded_bf16((B, H, 2 * n, D), seed, 4, device)
+        self.o = torch.empty_like(self.q)
+        self.lse = torch.empty((B, H, 2 * n), device=device, dtype=torch.float32)
+        self.dq, self.dk, self.dv = (torch.empty_like(self.q) for _ in range(3))
+        self.delta = torch.empty((B, H, 2 * n), device=device, dtype=torch.float32)
+        self.lib = lib()
+        self.fwd_strides = strides(self.q, self.k, self.v, self.o)
+        self.dq_strides = strides(self.q, self.k, self.v, self.o, self.do, self.dq)
+        self.dkdv_strides = strides(self.q, self.k, self.v, self.do, self.dk, self.dv)
+        self.stream = stream_of(self.q)
+        self.p = {name: ptr(getattr(self, name)) for name in
+                  ("q", "k", "v", "o", "lse", "do", "dq", "dk", "dv", "delta")}
+        self.scale = 1.0 / D ** 0.5
+
+    def fwd(self):
+        from kernels._native import check
+        p = self.p
+        check(self.lib.bd3_attn_fwd(p["q"], p["k"], p["v"], p["o"], p["lse"], self.B, self.H, self.n, D,
+                                    self.bs, self.fwd_strides, self.scale, self.stream))
+
+    def bwd_dq(self):
+        """bd3_attn_bwd_dq: dQ and Delta (first half of bd3_attn_bwd)."""
+        from kernels._native import check
+        p = self.p
+        check(self.lib.bd3_attn_bwd_dq(p["q"], p["k"], p["v"], p["o"], p["do"], p["lse"], p["dq"],
+                                       p["delta"], self.B, self.H, self.n, D, self.bs, self.dq_strides,
+                                       self.scale, self.stream))
+
+    def bwd_dkdv(self):
+        """bd3_attn_bwd_dkdv: dK, dV (second half of bd3_attn_bwd)."""
+        from kernels._native import check
+        p = self.p
+        check(self.lib.bd3_attn_bwd_dkdv(p["q"], p["k"], p["v"], p["do"], p["lse"], p["delta"], p["dk"],
+                                         p["dv"], self.B, self.H, self.n, D, self.bs, self.dkdv_strides,
+                                         self.scale, self.stream))
+
+    def bwd(self):
+        self.bwd_dq()
+        self.bwd_dkdv()
+
+    def useful_flops(self):
+        return 3.5 * useful_fwd_flops(self.B, self.H, self.n, self.bs)
+
+
+def time_train(step: TrainStep, steps: int, warmup: int):
+    """Warm up, then time exactly `steps` fwd+bwd steps: wall clock between
+    two synchronisations, plus HIP events around each of the step's three
+    launches (forward, dQ, dK/dV) on the stream the kernels run on.
+    Returns (ms per step, ms per launch of each kernel)."""
+    import torch
+    for _ in range(warmup):
+        step.fwd()
+        step.bwd()
+    torch.cuda.synchronize()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+    t0 = time.perf_counter()
+    for e in ev:
+        e[0].record()
+        step.fwd()
+        e[1].record()
+        step.bwd_dq()
+        e[2].record()
+        step.bwd_dkdv()
+        e[3].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = [sum(e[i].elapsed_time(e[i + 1]) for e in ev) / steps for i in range(3)]
+    return wall * 1e3 / steps, {"fwd": per[0], "bwd_dq": per[1], "bwd_dkdv": per[2]}
+
+
+def cpu_baseline(B, H, n, bs, budget_s: float):
+    """fp32 eager oracle fwd+bwd over (b, h) slices of the workload until the
+    budget is spent; value in useful TFLOP/s (same FLOP convention)."""
+    import torch
+    from oracle.attention import bd3_attention_grads
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    cores = max(1, min(cores, 16))
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(0)
+    q, k, v, do = (torch.randn(1, 1, 2 * n, D, generator=g).to(torch.bfloat16).float() for _ in range(4))
+    bd3_attention_grads(q, k, v, do, bs)  # warmup (allocations)
+    done, t0 = 0, time.perf_counter()
+    while True:
+        bd3_attention_grads(q, k, v, do, bs)
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or done >= B * H:
+            break
+    flops = 3.5 * useful_fwd_flops(1, 1, n, bs) * done
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": flops / el / 1e12,
+        "unit": "TFLOP/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"{done} of {B * H} (b,h) slices of the B={B} L={n} H={H} bs={bs} workload, "
+                   f"fp32 eager fwd+bwd (torch autograd, {cores} threads, {cpu_model}); "
+                   f"{el:.1f} s"),
+    }
+
+
+def decode_bench(device, reps: int):
+    """32 sequences x 12 heads, 16 queries over 4096 + 16 cached keys."""
+    import torch
+    from kernels._native import check, lib, ptr, stream_of, strides
+    from perf.harness import bench
+    B, H, q_len, kv_len, bs = 32, 12, 16, 4112, 16
+    q = seeded_bf16((B, H, q_len, D), 0, 1, device)[0]
+    k, v = seeded_bf16((B, H, kv_len, D), 1, 2, device)
+    o = torch.empty_like(q)
+    kv_bytes = 2 * B * H * kv_len * D * 2
+    st = strides(q, k, v, o)
+    stream = stream_of(q)
+    L = lib()
+    rows = []
+
+    def run(n_splits):
+        nbytes = L.bd3_decode_workspace_bytes(B, H, q_len, kv_len, D, n_splits)
+        ws = torch.empty(max(nbytes, 1), device=device, dtype=torch.uint8)
+
+        def call():
+            check(L.bd3_decode_splitkv(ptr(q), ptr(k), ptr(v), ptr(o), B, H, q_len, kv_len, D, bs,
+                                       n_splits, st, 1.0 / 8, ptr(ws), nbytes, stream))
+        return call
+
+    for ns in (1, 4, 8, 16, 0):
+        eff = ns if ns else -(-kv_len // 256)  # 0: the reference's SPLIT_N = 256 rule
+        t = bench(run(eff), warmup=5, rep=reps, flush=True)
+        rows.append({"n_splits": eff, "rule": "reference ceil(kv/256)" if ns == 0 else "explicit",
+                     "us": t.mean_ms * 1e3, "us_median": t.median_ms * 1e3,
+                     "GB_s": kv_bytes / (t.mean_ms * 1e-3) / 1e9})
+    # the library's auto split (bd3_decode)
+    nb_auto = L.bd3_decode_workspace_bytes(B, H, q_len, kv_len, D, 0)
+    ws_auto = torch.empty(max(nb_auto, 1), device=device, dtype=torch.uint8)
+    auto_splits = L.bd3_decode_auto_splits(B, H, q_len, kv_len)
+
+    def call_auto():
+        check(L.bd3_decode(ptr(q), ptr(k), ptr(v), ptr(o), B, H, q_len, kv_len, D, bs, st, 1.0 / 8,
+                           ptr(ws_auto), nb_auto, stream))
+    t = bench(call_auto, warmup=5, rep=reps, flush=True)
+    rows.append({"n_splits": auto_splits, "rule": "auto (bd3_decode)", "us": t.mean_ms * 1e3,
+                 "us_median": t.median_ms * 1e3, "GB_s": kv_bytes / (t.mean_ms * 1e-3) / 1e9})
+    best = max(rows, key=lambda r: r["GB_s"])
+    return {
+        "workload": "split-KV decode, 32 seq x 12 heads, q_len 16, kv_len 4112, d 64, bs 16, bf16",
+        "kv_bytes": kv_bytes,
+        "rows": rows,
+        "roofline": {"bound": "hbm", "achieved": best["GB_s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": best["GB_s"] / PEAK_HBM_GBS, "traffic": None,
+                     "kernel": f"bd3_decode_splitkv n_splits={best['n_splits']} ({best['rule']})"},
+    }
+
+
+def sweep_bench(device, steps: int):
+    """B=4, L=2048, H=16, block sizes {4, 16, 64, 256}."""
+    import torch
+    from kernels._native import lib
+    out = []
+    census = (ctypes.c_int64 * 6)()
+    for bs in (4, 16, 64, 256):
+        st = TrainStep(4, 16, 2048, bs, device)
+        ms, per = time_train(st, steps, 2)
+        lib().bd3_train_tile_census(2048, bs, census)
+        out.append({"block_size": bs, "ms": ms, "kernel_ms": per,
+                    "useful_tflops": st.useful_flops() / (ms * 1e-3) / 1e12,
+                    "frac_of_peak": st.useful_flops() / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+                    "useful_fraction_of_executed": census[0] / census[1]})
+        del st
+        torch.cuda.empty_cache()
+    return out
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-sweep", action="store_true")
+    args = ap.parse_args(argv)
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures the attention kernels on ONE GPU: the path has no "
+              "cross-GPU exchange to measure (each (batch, head) is independent); "
+              "run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+    from kernels._native import lib
+    metric = json.loads((REPO / "BASELINE.json").read_text())["metric"]
+    device = torch.device("cuda:0")
+    log(f"device: {torch.cuda.get_device_name(device)}")
+
+    B, H, n, bs = 8, 12, 1024, 16
+    step = TrainStep(B, H, n, bs, device)
+    ms, per = time_train(step, args.steps, args.warmup)
+    tflops = step.useful_flops() / (ms * 1e-3) / 1e12
+    log(f"config1 fwd+bwd: {ms * 1e3:.1f} us/step (fwd {per['fwd'] * 1e3:.1f} us, "
+        f"dQ {per['bwd_dq'] * 1e3:.1f} us, dK/dV {per['bwd_dkdv'] * 1e3:.1f} us) -> {tflops:.1f} useful TFLOP/s")
+
+    # Algorithmic FLOPs per launch: 2*d per live pair per matrix product the
+    # kernel must form (forward: S, PV; dQ kernel: S, dP, dQ; dK/dV kernel:
+    # S, dP, dV, dK).
+    fwd_flops = useful_fwd_flops(B, H, n, bs)
+    kernels = {
+        "attn_fwd_kernel (bd3_attn_fwd)": (fwd_flops, per["fwd"]),
+        "attn_bwd_dq_kernel (bd3_attn_bwd_dq)": (1.5 * fwd_flops, per["bwd_dq"]),
+        "attn_bwd_dkdv_kernel (bd3_attn_bwd_dkdv)": (2.0 * fwd_flops, per["bwd_dkdv"]),
+    }
+    dom_name, (dom_flops, dom_ms) = max(kernels.items(), key=lambda kv: kv[1][1])
+    achieved = dom_flops / (dom_ms * 1e-3) / 1e12
+    census = (ctypes.c_int64 * 6)()
+    lib().bd3_train_tile_census(n, bs, census)
+
+    result = {
+        "metric": metric,
+        "value": tflops,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: q, k, v, dO ~ N(0,1) from seed 0, bf16, resident in HBM",
+        "config": {"workload": "BD3-LM training attention fwd+bwd (configs[1])", "batch": B,
+                   "seq_len": n, "attn_seq": 2 * n, "heads": H, "head_dim": D, "block_size": bs},
+        "kernel_ms": per,
+        "kernel_tflops": {k: f / (t * 1e-3) / 1e12 for k, (f, t) in kernels.items()},
+        "useful_fraction_of_executed": census[0] / census[1],
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None, "kernel": dom_name,
+                     "algorithmic_flops_per_launch": dom_flops},
+    }
+    del step
+    torch.cuda.empty_cache()
+
+    if not args.no_decode:
+        result["decode"] = decode_bench(device, reps=30)
+        for r in result["decode"]["rows"]:
+            log(f"decode n_splits={r['n_splits']:3d} ({r['rule']}): {r['us']:.1f} us, {r['GB_s']:.0f} GB/s")
+    if not args.no_sweep:
+        result["sweep"] = sweep_bench(device, steps=10)
+        for r in result["sweep"]:
+            log(f"sweep bs={r['block_size']:3d}: {r['ms'] * 1e3:.1f} us, {r['useful_tflops']:.1f} TFLOP/s")
+    if not args.no_cpu_baseline:
+        log("cpu baseline ...")
+        result["cpu_baseline"] = cpu_baseline(B, H, n, bs, args.cpu_budget)
+        log(f"cpu baseline: {result['cpu_baseline']['value'] * 1e3:.2f} GFLOP/s "
+            f"({result['cpu_baseline']['sample']})")
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

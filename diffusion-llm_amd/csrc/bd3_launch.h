@@ -40,8 +40,7 @@ struct BwdArgs {
   uint16_t* dq;
   uint16_t* dk;
   uint16_t* dv;
-  float* delta;   // workspace (B, H, 2n)
-  float* dq_acc;  // workspace (B, H, 2n, 64), fp32
+  float* delta;  // (B, H, 2n) fp32: written by the dQ kernel, read by dK/dV
   Strides3 sq, sk, sv, so, sdo, sdq, sdk, sdv;
   int heads;
   int bh;
@@ -71,7 +70,8 @@ struct DecodeArgs {
 };
 
 hipError_t launch_attn_fwd(const FwdArgs& a, hipStream_t stream);
-hipError_t launch_attn_bwd(const BwdArgs& a, hipStream_t stream);
+hipError_t launch_attn_bwd_dq(const BwdArgs& a, hipStream_t stream);
+hipError_t launch_attn_bwd_dkdv(const BwdArgs& a, hipStream_t stream);
 hipError_t launch_decode(const DecodeArgs& a, int qt, hipStream_t stream);
 hipError_t launch_mask_dump(uint8_t* out, int mode, int rows, int kv_len,
                             int bs, hipStream_t stream);

@@ -81,6 +81,28 @@ BD3_HD RowIntervals train_row_intervals(int q, int n, int bs) {
   return r;
 }
 
+// Rows that see training key k (global index), as two half-open row
+// intervals: the transpose of train_row_intervals.
+//   noisy key, block b: noisy rows of block b;
+//   clean key, block b: noisy rows of blocks > b and clean rows of blocks >= b.
+BD3_HD RowIntervals train_col_intervals(int k, int n, int bs) {
+  RowIntervals r;
+  if (k < n) {
+    const int b = k / bs;
+    r.lo1 = bs * b;
+    r.hi1 = imin(bs * (b + 1), n);
+    r.lo2 = 0;
+    r.hi2 = 0;
+  } else {
+    const int b = (k - n) / bs;
+    r.lo1 = imin(bs * (b + 1), n);
+    r.hi1 = n;
+    r.lo2 = n + bs * b;
+    r.hi2 = 2 * n;
+  }
+  return r;
+}
+
 BD3_HD bool row_sees(const RowIntervals& r, int k) {
   return (k >= r.lo1 && k < r.hi1) || (k >= r.lo2 && k < r.hi2);
 }

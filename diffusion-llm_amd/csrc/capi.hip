@@ -71,6 +71,41 @@ int check_common_decode(const void* q, const void* k, const void* v, void* o, in
   return BD3_OK;
 }
 
+int check_bwd_shape(int batch, int heads, int n, int head_dim, int block_size,
+                    const int64_t* strides) {
+  if (batch < 1 || heads < 1) return fail(BD3_EINVAL, "batch and heads must be >= 1");
+  if (head_dim != bd3::kHeadDim) return fail(BD3_EINVAL, "head_dim must be 64, got %d", head_dim);
+  if (n < 128 || n % 128 != 0)
+    return fail(BD3_EINVAL, "n (half the sequence) must be a positive multiple of 128, got %d", n);
+  if (block_size < 1 || n % block_size != 0)
+    return fail(BD3_EINVAL, "n (%d) must be a multiple of block_size (%d)", n, block_size);
+  if (strides == nullptr) return fail(BD3_EINVAL, "strides is NULL");
+  return BD3_OK;
+}
+
+bd3::BwdArgs bwd_args(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                      const float* lse, void* dq, void* dk, void* dv, float* delta, int batch,
+                      int heads, int n, int block_size, float scale) {
+  bd3::BwdArgs a = {};
+  a.q = static_cast<const uint16_t*>(q);
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.o = static_cast<const uint16_t*>(o);
+  a.dout = static_cast<const uint16_t*>(dout);
+  a.lse = lse;
+  a.dq = static_cast<uint16_t*>(dq);
+  a.dk = static_cast<uint16_t*>(dk);
+  a.dv = static_cast<uint16_t*>(dv);
+  a.delta = delta;
+  a.heads = heads;
+  a.bh = batch * heads;
+  a.n = n;
+  a.bs = block_size;
+  a.scale = scale;
+  a.scale_log2 = scale * bd3::kLog2e;
+  return a;
+}
+
 int32_t auto_splits(int32_t batch, int32_t heads, int32_t q_len, int32_t kv_len) {
   // Aim for about four workgroups per CU on a 256-CU part, never fewer than
   // 128 keys per split, and never more than the reference's rule would use.
@@ -165,8 +200,52 @@ int bd3_attn_fwd(const void* q, const void* k, const void* v, void* o, float* ls
 
 size_t bd3_attn_bwd_workspace_bytes(int32_t batch, int32_t heads, int32_t n, int32_t head_dim) {
   if (batch < 1 || heads < 1 || n < 1 || head_dim < 1) return 0;
-  const size_t rows = (size_t)batch * heads * 2 * n;
-  return align256(rows * sizeof(float)) + align256(rows * head_dim * sizeof(float));
+  return align256((size_t)batch * heads * 2 * n * sizeof(float));  // Delta
+}
+
+int bd3_attn_bwd_dq(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                    const float* lse, void* dq, float* delta, int32_t batch, int32_t heads, int32_t n,
+                    int32_t head_dim, int32_t block_size, const int64_t* strides, float scale,
+                    void* stream) {
+  int st = check_bwd_shape(batch, heads, n, head_dim, block_size, strides);
+  if (st) return st;
+  const char* names[6] = {"q", "k", "v", "o", "dout", "dq"};
+  const void* ptrs[6] = {q, k, v, o, dout, dq};
+  for (int i = 0; i < 6; ++i)
+    if ((st = check_tensor(ptrs[i], strides + 3 * i, names[i]))) return st;
+  if (lse == nullptr || delta == nullptr) return fail(BD3_EINVAL, "lse and delta must be non-NULL");
+  bd3::BwdArgs a = bwd_args(q, k, v, o, dout, lse, dq, nullptr, nullptr, delta, batch, heads, n,
+                            block_size, scale);
+  a.sq = s3(strides);
+  a.sk = s3(strides + 3);
+  a.sv = s3(strides + 6);
+  a.so = s3(strides + 9);
+  a.sdo = s3(strides + 12);
+  a.sdq = s3(strides + 15);
+  return hip_status(bd3::launch_attn_bwd_dq(a, static_cast<hipStream_t>(stream)), "attn_bwd_dq launch");
+}
+
+int bd3_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* dout, const float* lse,
+                      const float* delta, void* dk, void* dv, int32_t batch, int32_t heads, int32_t n,
+                      int32_t head_dim, int32_t block_size, const int64_t* strides, float scale,
+                      void* stream) {
+  int st = check_bwd_shape(batch, heads, n, head_dim, block_size, strides);
+  if (st) return st;
+  const char* names[6] = {"q", "k", "v", "dout", "dk", "dv"};
+  const void* ptrs[6] = {q, k, v, dout, dk, dv};
+  for (int i = 0; i < 6; ++i)
+    if ((st = check_tensor(ptrs[i], strides + 3 * i, names[i]))) return st;
+  if (lse == nullptr || delta == nullptr) return fail(BD3_EINVAL, "lse and delta must be non-NULL");
+  bd3::BwdArgs a = bwd_args(q, k, v, nullptr, dout, lse, nullptr, dk, dv, const_cast<float*>(delta),
+                            batch, heads, n, block_size, scale);
+  a.sq = s3(strides);
+  a.sk = s3(strides + 3);
+  a.sv = s3(strides + 6);
+  a.sdo = s3(strides + 9);
+  a.sdk = s3(strides + 12);
+  a.sdv = s3(strides + 15);
+  return hip_status(bd3::launch_attn_bwd_dkdv(a, static_cast<hipStream_t>(stream)),
+                    "attn_bwd_dkdv launch");
 }
 
 int bd3_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
@@ -174,51 +253,28 @@ int bd3_attn_bwd(const void* q, const void* k, const void* v, const void* o, con
                  size_t workspace_bytes, int32_t batch, int32_t heads, int32_t n,
                  int32_t head_dim, int32_t block_size, const int64_t* strides, float scale,
                  void* stream) {
-  if (batch < 1 || heads < 1) return fail(BD3_EINVAL, "batch and heads must be >= 1");
-  if (head_dim != bd3::kHeadDim) return fail(BD3_EINVAL, "head_dim must be 64, got %d", head_dim);
-  if (n < 128 || n % 128 != 0)
-    return fail(BD3_EINVAL, "n (half the sequence) must be a positive multiple of 128, got %d", n);
-  if (block_size < 1 || n % block_size != 0)
-    return fail(BD3_EINVAL, "n (%d) must be a multiple of block_size (%d)", n, block_size);
-  if (strides == nullptr) return fail(BD3_EINVAL, "strides is NULL");
+  int st = check_bwd_shape(batch, heads, n, head_dim, block_size, strides);
+  if (st) return st;
   const char* names[8] = {"q", "k", "v", "o", "dout", "dq", "dk", "dv"};
   const void* ptrs[8] = {q, k, v, o, dout, dq, dk, dv};
-  for (int i = 0; i < 8; ++i) {
-    int st = check_tensor(ptrs[i], strides + 3 * i, names[i]);
-    if (st) return st;
-  }
+  for (int i = 0; i < 8; ++i)
+    if ((st = check_tensor(ptrs[i], strides + 3 * i, names[i]))) return st;
   if (lse == nullptr) return fail(BD3_EINVAL, "lse is NULL");
   const size_t need = bd3_attn_bwd_workspace_bytes(batch, heads, n, head_dim);
   if (workspace == nullptr || !aligned16(workspace) || workspace_bytes < need)
     return fail(BD3_EINVAL, "workspace must be a 16-byte aligned buffer of >= %zu bytes", need);
-  const size_t rows = (size_t)batch * heads * 2 * n;
-  bd3::BwdArgs a;
-  a.q = static_cast<const uint16_t*>(q);
-  a.k = static_cast<const uint16_t*>(k);
-  a.v = static_cast<const uint16_t*>(v);
-  a.o = static_cast<const uint16_t*>(o);
-  a.dout = static_cast<const uint16_t*>(dout);
-  a.lse = lse;
-  a.dq = static_cast<uint16_t*>(dq);
-  a.dk = static_cast<uint16_t*>(dk);
-  a.dv = static_cast<uint16_t*>(dv);
-  a.delta = static_cast<float*>(workspace);
-  a.dq_acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + align256(rows * sizeof(float)));
-  a.sq = s3(strides);
-  a.sk = s3(strides + 3);
-  a.sv = s3(strides + 6);
-  a.so = s3(strides + 9);
-  a.sdo = s3(strides + 12);
-  a.sdq = s3(strides + 15);
-  a.sdk = s3(strides + 18);
-  a.sdv = s3(strides + 21);
-  a.heads = heads;
-  a.bh = batch * heads;
-  a.n = n;
-  a.bs = block_size;
-  a.scale = scale;
-  a.scale_log2 = scale * bd3::kLog2e;
-  return hip_status(bd3::launch_attn_bwd(a, static_cast<hipStream_t>(stream)), "attn_bwd launch");
+  // q, k, v, o, dout, dq | q, k, v, dout, dk, dv
+  const int64_t* S = strides;
+  const int64_t dq_strides[18] = {S[0],  S[1],  S[2],  S[3],  S[4],  S[5],  S[6],  S[7],  S[8],
+                                  S[9],  S[10], S[11], S[12], S[13], S[14], S[15], S[16], S[17]};
+  const int64_t kv_strides[18] = {S[0],  S[1],  S[2],  S[3],  S[4],  S[5],  S[6],  S[7],  S[8],
+                                  S[12], S[13], S[14], S[18], S[19], S[20], S[21], S[22], S[23]};
+  float* delta = static_cast<float*>(workspace);
+  st = bd3_attn_bwd_dq(q, k, v, o, dout, lse, dq, delta, batch, heads, n, head_dim, block_size,
+                       dq_strides, scale, stream);
+  if (st) return st;
+  return bd3_attn_bwd_dkdv(q, k, v, dout, lse, delta, dk, dv, batch, heads, n, head_dim, block_size,
+                           kv_strides, scale, stream);
 }
 
 int32_t bd3_decode_auto_splits(int32_t batch, int32_t heads, int32_t q_len, int32_t kv_len) {
@@ -228,7 +284,7 @@ int32_t bd3_decode_auto_splits(int32_t batch, int32_t heads, int32_t q_len, int3
 
 size_t bd3_decode_workspace_bytes(int32_t batch, int32_t heads, int32_t q_len, int32_t kv_len,
                                   int32_t head_dim, int32_t n_splits) {
-  if (batch < 1 || heads < 1 || q_len < 1 || kv_len < 1) return 0;
+  if (batch < 1 || heads < 1 || q_len < 1 || kv_len < 1 || n_splits < 0) return 0;
   if (n_splits == 0) n_splits = auto_splits(batch, heads, q_len, kv_len);
   if (n_splits <= 1) return 0;
   const size_t slots = (size_t)batch * heads * decode_q_tiles(q_len) * n_splits * kDecodeQT;
@@ -252,7 +308,6 @@ int bd3_decode_splitkv(const void* q, const void* k, const void* v, void* o, int
                        void* workspace, size_t workspace_bytes, void* stream) {
   int st = check_common_decode(q, k, v, o, batch, heads, q_len, kv_len, head_dim, block_size, strides);
   if (st) return st;
-  if (n_splits == 0) n_splits = (kv_len + 255) / 256;  // reference SPLIT_N = 256 rule
   if (n_splits < 1 || n_splits > kv_len)
     return fail(BD3_EINVAL, "n_splits must be in [1, kv_len], got %d", n_splits);
   return run_decode(q, k, v, o, batch, heads, q_len, kv_len, block_size, n_splits, strides, scale,
@@ -279,6 +334,18 @@ int bd3_train_classify(int32_t n, int32_t block_size, int32_t q0, int32_t k0) {
   if (n < 32 || n % 32 != 0 || block_size < 1) return -1;
   if (q0 < 0 || k0 < 0 || q0 + 32 > 2 * n || k0 + 32 > 2 * n || q0 % 32 || k0 % 32) return -1;
   return bd3::train_class(q0, 32, k0, 32, n, block_size);
+}
+
+int bd3_train_intervals(int32_t n, int32_t block_size, int32_t index, int32_t mode, int32_t* out) {
+  if (out == nullptr || n < 1 || block_size < 1 || index < 0 || index >= 2 * n) return -1;
+  if (mode != 0 && mode != 1) return -1;
+  const bd3::RowIntervals r = mode == 0 ? bd3::train_row_intervals(index, n, block_size)
+                                        : bd3::train_col_intervals(index, n, block_size);
+  out[0] = r.lo1;
+  out[1] = r.hi1;
+  out[2] = r.lo2;
+  out[3] = r.hi2;
+  return 0;
 }
 
 int bd3_train_tile_census(int32_t n, int32_t block_size, int64_t* out) {

@@ -34,6 +34,10 @@ SIGNATURES: dict[str, tuple] = {
     "bd3_attn_bwd_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32]),
     "bd3_attn_bwd": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _sz,
                                     _i32, _i32, _i32, _i32, _i32, _i64p, _f32, _c_p]),
+    "bd3_attn_bwd_dq": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _i32, _i32, _i32,
+                                       _i32, _i32, _i64p, _f32, _c_p]),
+    "bd3_attn_bwd_dkdv": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _i32, _i32, _i32,
+                                         _i32, _i32, _i64p, _f32, _c_p]),
     "bd3_decode": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i32,
                                   _i64p, _f32, _c_p, _sz, _c_p]),
     "bd3_decode_auto_splits": (_i32, [_i32, _i32, _i32, _i32]),
@@ -43,6 +47,7 @@ SIGNATURES: dict[str, tuple] = {
     "bd3_mask_dump": (ctypes.c_int, [_c_p, _i32, _i32, _i32, _i32, _c_p]),
     "bd3_train_tile_census": (ctypes.c_int, [_i32, _i32, _i64p]),
     "bd3_train_classify": (ctypes.c_int, [_i32, _i32, _i32, _i32]),
+    "bd3_train_intervals": (ctypes.c_int, [_i32, _i32, _i32, _i32, ctypes.POINTER(ctypes.c_int32)]),
 }
 
 _lib = None

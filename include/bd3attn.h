@@ -69,27 +69,24 @@ int bd3_attn_fwd(const void* q, const void* k, const void* v, void* o,
                  float scale, void* stream);
 
 /*
- * Bytes of workspace bd3_attn_bwd needs: Delta = rowsum(dO * O) and an
- * fp32 dQ accumulator, both (batch, heads, 2n[, head_dim]).
- * No reference counterpart (the reference allocates with torch.empty).
+ * Bytes of workspace bd3_attn_bwd needs: Delta = rowsum(dO * O), fp32,
+ * (batch, heads, 2n). No reference counterpart (the reference allocates
+ * Delta with a torch op, kernels/BlockSparseFlashAttention.py:525).
  */
 size_t bd3_attn_bwd_workspace_bytes(int32_t batch, int32_t heads, int32_t n,
                                     int32_t head_dim);
 
 /*
  * Training attention backward: dQ, dK, dV of the forward above, given
- * dO and the forward's O and lse. Delta = rowsum(dO * O) is computed
- * inside (fused preprocess).
+ * dO and the forward's O and lse. Runs bd3_attn_bwd_dq then
+ * bd3_attn_bwd_dkdv with Delta in the workspace.
  * strides: 24 int64 = (b, h, s) element strides of
  *          q, k, v, o, dout, dq, dk, dv.
- * Preconditions: as the forward, plus n % block_size == 0 and
- * workspace_bytes >= bd3_attn_bwd_workspace_bytes(...).
+ * Preconditions: as the forward, plus n % block_size == 0 (the reference
+ * asserts it, :522) and workspace_bytes >= bd3_attn_bwd_workspace_bytes().
  *
- * Replaces the Delta torch op and the launches of
- * block_sparse_attention_bwd_dq_kern and
- * block_sparse_attention_dk_dv_bwd_kern in
- * BlockSparseFlashAttention.backward
- * (kernels/BlockSparseFlashAttention.py:508-562; kernels :212-328, :368-452).
+ * Replaces BlockSparseFlashAttention.backward's device work
+ * (kernels/BlockSparseFlashAttention.py:508-562).
  */
 int bd3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
                  const void* dout, const float* lse, void* dq, void* dk,
@@ -97,6 +94,37 @@ int bd3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
                  int32_t batch, int32_t heads, int32_t n, int32_t head_dim,
                  int32_t block_size, const int64_t* strides, float scale,
                  void* stream);
+
+/*
+ * Backward, first stage: dQ = scale * dS K with dS = P o (dP - Delta),
+ * and Delta = rowsum(dO * O) written to `delta` (fp32, contiguous
+ * (batch, heads, 2n)) for the second stage.
+ * strides: 18 int64 = (b, h, s) element strides of q, k, v, o, dout, dq.
+ * Preconditions: as bd3_attn_bwd.
+ *
+ * Replaces the Delta torch op (kernels/BlockSparseFlashAttention.py:525)
+ * and block_sparse_attention_bwd_dq_kern with its launch (:368-452, :532-543).
+ */
+int bd3_attn_bwd_dq(const void* q, const void* k, const void* v,
+                    const void* o, const void* dout, const float* lse,
+                    void* dq, float* delta, int32_t batch, int32_t heads,
+                    int32_t n, int32_t head_dim, int32_t block_size,
+                    const int64_t* strides, float scale, void* stream);
+
+/*
+ * Backward, second stage: dV = P^T dO and dK = scale * dS^T Q, given the
+ * Delta the first stage wrote.
+ * strides: 18 int64 = (b, h, s) element strides of q, k, v, dout, dk, dv.
+ * Preconditions: as bd3_attn_bwd.
+ *
+ * Replaces block_sparse_attention_dk_dv_bwd_kern and its launch
+ * (kernels/BlockSparseFlashAttention.py:212-328, :545-560).
+ */
+int bd3_attn_bwd_dkdv(const void* q, const void* k, const void* v,
+                      const void* dout, const float* lse, const float* delta,
+                      void* dk, void* dv, int32_t batch, int32_t heads,
+                      int32_t n, int32_t head_dim, int32_t block_size,
+                      const int64_t* strides, float scale, void* stream);
 
 /*
  * Block-sparse decode attention: queries are the LAST q_len of kv_len
@@ -126,7 +154,8 @@ int32_t bd3_decode_auto_splits(int32_t batch, int32_t heads, int32_t q_len,
                                int32_t kv_len);
 
 /*
- * Workspace bytes for a split-KV decode with n_splits splits (0 = auto):
+ * Workspace bytes for a split-KV decode with n_splits splits (0 = the auto
+ * count bd3_decode uses):
  * fp32 partial O and LSE per (batch*head, query tile, split). 0 when a
  * single split needs no workspace. No reference counterpart (the
  * reference allocates o_part / lse with torch.empty,
@@ -140,7 +169,8 @@ size_t bd3_decode_workspace_bytes(int32_t batch, int32_t heads, int32_t q_len,
  * Split-KV decode attention: the keys [0, kv_len) are cut into n_splits
  * contiguous ranges, each producing a normalised fp32 partial O and its
  * LSE, merged with LSE weights (FlashDecoding). Same result as bd3_decode.
- * n_splits = 0 means the reference rule ceil(kv_len / 256).
+ * The reference's default split count is ceil(kv_len / 256)
+ * (kernels/SplitKVDecodeAttention.py:147); callers pass it explicitly.
  * strides: 12 int64 = (b, h, s) element strides of q, k, v, o.
  * Preconditions: 1 <= q_len <= kv_len, head_dim == 64,
  * 1 <= n_splits <= kv_len, workspace large enough.
@@ -183,6 +213,15 @@ int bd3_train_tile_census(int32_t n, int32_t block_size, int64_t* out);
  * 0 = no live pair, 1 = every pair live, 2 = partial. For CPU tests.
  */
 int bd3_train_classify(int32_t n, int32_t block_size, int32_t q0, int32_t k0);
+
+/*
+ * Host-only: the interval form of the training mask the kernels apply inside
+ * partial blocks, for CPU tests. mode 0: the keys row `index` sees; mode 1:
+ * the rows that see key `index`. Writes out[0..3] = {lo1, hi1, lo2, hi2}:
+ * the set is [lo1, hi1) union [lo2, hi2). Returns 0, or -1 on bad arguments.
+ */
+int bd3_train_intervals(int32_t n, int32_t block_size, int32_t index,
+                        int32_t mode, int32_t* out);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,155 @@
+"""The C-ABI library on a machine without a GPU: it loads, exports every
+symbol include/bd3attn.h declares, its host-only census/classification
+agree with the mask oracle, and every precondition violation returns
+BD3_EINVAL with a message before any HIP call."""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from kernels import _native
+from oracle.mask import block_diff_mask
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "bd3attn.h"
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _native.LIB_PATH.exists():
+        import __graft_entry__
+        __graft_entry__.build()
+    return _native.lib()
+
+
+def header_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(bd3_\w+)\s*\(", text)))
+
+
+def test_exports_every_declared_symbol(lib):
+    names = header_functions()
+    assert len(names) >= 12
+    for name in names:
+        assert hasattr(lib, name), f"{name} not exported"
+    assert sorted(_native.SIGNATURES) == names, "ctypes table out of sync with the header"
+
+
+def test_abi_version(lib):
+    assert lib.bd3_abi_version() == 1
+
+
+@pytest.mark.parametrize("n,bs", [(128, 1), (128, 16), (256, 4), (256, 100), (384, 64), (512, 512),
+                                  (1024, 16), (2048, 256)])
+def test_census_matches_oracle(lib, n, bs):
+    out = (ctypes.c_int64 * 6)()
+    assert lib.bd3_train_tile_census(n, bs, out) == 0
+    m = block_diff_mask(n, bs)
+    assert out[0] == int(m.sum())            # useful pairs
+    if n % bs == 0:
+        assert out[5] == out[0] == n * n + n * bs
+    assert out[1] >= out[0]                  # executed covers useful
+    assert out[1] == 1024 * (out[2] + out[3])
+
+
+@pytest.mark.parametrize("n,bs", [(64, 1), (64, 16), (96, 7), (128, 32), (128, 128), (160, 64)])
+def test_classification_exact(lib, n, bs):
+    """none = no live pair, full = all live, partial = mixed, for every
+    (32-row group, 32-key sub-block)."""
+    m = block_diff_mask(n, bs)
+    for q0 in range(0, 2 * n, 32):
+        for k0 in range(0, 2 * n, 32):
+            blk = m[q0:q0 + 32, k0:k0 + 32]
+            c = lib.bd3_train_classify(n, bs, q0, k0)
+            want = 0 if not blk.any() else (1 if blk.all() else 2)
+            assert c == want, (q0, k0)
+
+
+@pytest.mark.parametrize("n,bs", [(8, 1), (8, 3), (64, 16), (96, 7), (128, 128), (256, 64)])
+def test_interval_forms_match_mask(lib, n, bs):
+    """The row intervals (forward, dQ kernels) and column intervals (dK/dV
+    kernel) reproduce every row and column of block_diff_mask."""
+    m = block_diff_mask(n, bs)
+    out = (ctypes.c_int32 * 4)()
+    idx = np.arange(2 * n)
+    for i in range(2 * n):
+        for mode, want in ((0, m[i, :]), (1, m[:, i])):
+            assert lib.bd3_train_intervals(n, bs, i, mode, out) == 0
+            lo1, hi1, lo2, hi2 = list(out)
+            got = ((idx >= lo1) & (idx < hi1)) | ((idx >= lo2) & (idx < hi2))
+            assert np.array_equal(got, want), (mode, i)
+
+
+def _i64(vals):
+    return (ctypes.c_int64 * len(vals))(*vals)
+
+
+GOOD = 0x100000  # a 16-byte aligned fake device address: never dereferenced,
+                 # every call below fails validation before any HIP call
+
+
+def expect_einval(status, fragment):
+    assert status == _native.BD3_EINVAL
+    assert fragment in _native.last_error()
+
+
+def test_fwd_validation(lib):
+    st = _i64([8 * 64 * 256] * 0 + [64 * 256, 64 * 256, 64] * 4)
+    expect_einval(lib.bd3_attn_fwd(GOOD, GOOD, GOOD, GOOD, GOOD, 1, 1, 100, 64, 16, st, 0.125, None),
+                  "multiple of 128")
+    expect_einval(lib.bd3_attn_fwd(GOOD, GOOD, GOOD, GOOD, GOOD, 1, 1, 128, 128, 16, st, 0.125, None),
+                  "head_dim")
+    expect_einval(lib.bd3_attn_fwd(GOOD, GOOD, GOOD, GOOD, GOOD, 1, 1, 128, 64, 0, st, 0.125, None),
+                  "block_size")
+    expect_einval(lib.bd3_attn_fwd(None, GOOD, GOOD, GOOD, GOOD, 1, 1, 128, 64, 16, st, 0.125, None),
+                  "q is NULL")
+    expect_einval(lib.bd3_attn_fwd(GOOD, GOOD + 2, GOOD, GOOD, GOOD, 1, 1, 128, 64, 16, st, 0.125, None),
+                  "aligned")
+    bad = _i64([64 * 256, 64 * 256, 63] + [64 * 256, 64 * 256, 64] * 3)
+    expect_einval(lib.bd3_attn_fwd(GOOD, GOOD, GOOD, GOOD, GOOD, 1, 1, 128, 64, 16, bad, 0.125, None),
+                  "stride")
+    expect_einval(lib.bd3_attn_fwd(GOOD, GOOD, GOOD, GOOD, None, 1, 1, 128, 64, 16, st, 0.125, None),
+                  "lse")
+
+
+def test_bwd_validation(lib):
+    st = _i64([64 * 256, 64 * 256, 64] * 8)
+    need = lib.bd3_attn_bwd_workspace_bytes(1, 1, 128, 64)
+    assert need == 1 * 1 * 256 * 4  # Delta
+    args = [GOOD] * 9
+    expect_einval(lib.bd3_attn_bwd(*args, GOOD, need, 1, 1, 128, 64, 3, st, 0.125, None), "multiple of block_size")
+    expect_einval(lib.bd3_attn_bwd(*args, GOOD, need - 1, 1, 1, 128, 64, 16, st, 0.125, None), "workspace")
+    expect_einval(lib.bd3_attn_bwd(*args, None, need, 1, 1, 128, 64, 16, st, 0.125, None), "workspace")
+    st18 = _i64([64 * 256, 64 * 256, 64] * 6)
+    expect_einval(lib.bd3_attn_bwd_dq(*[GOOD] * 7, None, 1, 1, 128, 64, 16, st18, 0.125, None), "delta")
+    expect_einval(lib.bd3_attn_bwd_dkdv(*[GOOD] * 8, 1, 1, 128, 64, 5, st18, 0.125, None), "block_size")
+    expect_einval(lib.bd3_attn_bwd_dkdv(GOOD, GOOD, GOOD, GOOD + 8, *[GOOD] * 4, 1, 1, 128, 64, 16, st18,
+                                        0.125, None), "dout")
+
+
+def test_decode_validation(lib):
+    st = _i64([64 * 64, 64 * 64, 64] * 4)
+    expect_einval(lib.bd3_decode(GOOD, GOOD, GOOD, GOOD, 1, 1, 33, 32, 64, 16, st, 0.125, GOOD, 0, None),
+                  "q_len")
+    expect_einval(lib.bd3_decode_splitkv(GOOD, GOOD, GOOD, GOOD, 1, 1, 16, 32, 64, 16, 0, st, 0.125, GOOD,
+                                         1 << 20, None), "n_splits")
+    expect_einval(lib.bd3_decode_splitkv(GOOD, GOOD, GOOD, GOOD, 1, 1, 16, 32, 64, 16, 33, st, 0.125, GOOD,
+                                         1 << 20, None), "n_splits")
+    need = lib.bd3_decode_workspace_bytes(1, 1, 16, 32, 64, 2)
+    expect_einval(lib.bd3_decode_splitkv(GOOD, GOOD, GOOD, GOOD, 1, 1, 16, 32, 64, 16, 2, st, 0.125, GOOD,
+                                         need - 1, None), "workspace")
+    expect_einval(lib.bd3_mask_dump(GOOD, 2, 4, 4, 1, None), "mode")
+    expect_einval(lib.bd3_mask_dump(GOOD, 1, 5, 4, 1, None), "q_len")
+
+
+def test_workspace_sizes(lib):
+    # one split needs no workspace; partials are (BH, q_tiles, splits, 32, 64) fp32 + LSE
+    assert lib.bd3_decode_workspace_bytes(2, 3, 16, 100, 64, 1) == 0
+    slots = 2 * 3 * 1 * 4 * 32
+    assert lib.bd3_decode_workspace_bytes(2, 3, 16, 100, 64, 4) == slots * 64 * 4 + ((slots * 4 + 255) // 256) * 256
+    s = lib.bd3_decode_auto_splits(32, 12, 16, 4112)
+    assert 1 <= s <= 4112 // 128
+    assert lib.bd3_decode_workspace_bytes(32, 12, 16, 4112, 64, 0) == lib.bd3_decode_workspace_bytes(
+        32, 12, 16, 4112, 64, s)
