@@ -40,7 +40,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_bwd_dq_kernel(BwdArgs a) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = wave_uniform(tid >> 6);
   const int l32 = lane & 31;
   const int g = lane >> 5;
 
@@ -80,9 +80,10 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_bwd_dq_kernel(BwdArgs a) {
   }
 
   const KeyRanges kr = train_key_ranges(q0, kBM, a.n, a.bs, kTileRows);
-  const int n_first = kr.t1 - kr.t0;
-  const int n_tiles = n_first + (kr.t3 - kr.t2);
-  auto tile_of = [&](int i) { return i < n_first ? kr.t0 + i : kr.t2 + (i - n_first); };
+  const int t0 = wave_uniform(kr.t0), t2 = wave_uniform(kr.t2);
+  const int n_first = wave_uniform(kr.t1 - kr.t0);
+  const int n_tiles = n_first + wave_uniform(kr.t3 - kr.t2);
+  auto tile_of = [&](int i) { return i < n_first ? t0 + i : t2 + (i - n_first); };
 
   TileStager<kThreads, 2> st;
   {
@@ -99,7 +100,8 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_bwd_dq_kernel(BwdArgs a) {
 #pragma unroll
   for (int qb = 0; qb < RB; ++qb) dq[qb][0] = dq[qb][1] = f32x16{};
 
-  if (n_tiles > 0) {
+  // n_tiles >= 1 (every row group sees its own block): unconditional prologue.
+  {
     stage_load(0);
     __bf16* dst[2] = {smem[0][0], smem[0][1]};
     st.store(dst);
@@ -109,7 +111,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_bwd_dq_kernel(BwdArgs a) {
   for (int it = 0; it < n_tiles; ++it) {
     const int stage = it & 1;
     if (it + 1 < n_tiles) stage_load(it + 1);
-    const int k0 = tile_of(it) * kTileRows;
+    const int k0 = wave_uniform(tile_of(it) * kTileRows);
     const __bf16* ks = smem[stage][0];
     const __bf16* vs = smem[stage][1];
 
@@ -119,7 +121,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_bwd_dq_kernel(BwdArgs a) {
     for (int qb = 0; qb < RB; ++qb)
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb) {
-        cls[qb][sb] = train_class(qrow0 + 32 * qb, 32, k0 + 32 * sb, 32, a.n, a.bs);
+        cls[qb][sb] = wave_uniform(train_class(qrow0 + 32 * qb, 32, k0 + 32 * sb, 32, a.n, a.bs));
         live[sb] |= cls[qb][sb];
       }
 
@@ -209,7 +211,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_bwd_dkdv_kernel(BwdArgs a) 
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = wave_uniform(tid >> 6);
   const int l32 = lane & 31;
   const int g = lane >> 5;
 
@@ -239,9 +241,10 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_bwd_dkdv_kernel(BwdArgs a) 
   }
 
   const KeyRanges qr = train_query_ranges(k0, kBK, a.n, a.bs, kTileRows);
-  const int n_first = qr.t1 - qr.t0;
-  const int n_tiles = n_first + (qr.t3 - qr.t2);
-  auto tile_of = [&](int i) { return i < n_first ? qr.t0 + i : qr.t2 + (i - n_first); };
+  const int t0 = wave_uniform(qr.t0), t2 = wave_uniform(qr.t2);
+  const int n_first = wave_uniform(qr.t1 - qr.t0);
+  const int n_tiles = n_first + wave_uniform(qr.t3 - qr.t2);
+  auto tile_of = [&](int i) { return i < n_first ? t0 + i : t2 + (i - n_first); };
 
   TileStager<kThreads, 2> st;
   {
@@ -271,16 +274,15 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_bwd_dkdv_kernel(BwdArgs a) 
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb) dk[kb][0] = dk[kb][1] = dv[kb][0] = dv[kb][1] = f32x16{};
 
-  if (n_tiles > 0) {
-    stage_load(0);
-    stage_store(0);
-  }
+  // n_tiles >= 1 (every key group is seen by its own block): unconditional prologue.
+  stage_load(0);
+  stage_store(0);
   __syncthreads();
 
   for (int it = 0; it < n_tiles; ++it) {
     const int stage = it & 1;
     if (it + 1 < n_tiles) stage_load(it + 1);
-    const int q0 = tile_of(it) * kTileRows;
+    const int q0 = wave_uniform(tile_of(it) * kTileRows);
     const __bf16* qs = smem[stage][0];
     const __bf16* dos = smem[stage][1];
 
@@ -290,7 +292,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_bwd_dkdv_kernel(BwdArgs a) 
     for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
-        cls[qb][kb] = train_class(q0 + 32 * qb, 32, kw + 32 * kb, 32, a.n, a.bs);
+        cls[qb][kb] = wave_uniform(train_class(q0 + 32 * qb, 32, kw + 32 * kb, 32, a.n, a.bs));
         live[qb] |= cls[qb][kb];
       }
 

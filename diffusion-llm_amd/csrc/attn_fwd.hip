@@ -43,7 +43,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_kernel(FwdArgs a) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = wave_uniform(tid >> 6);
   const int l32 = lane & 31;
   const int g = lane >> 5;
 
@@ -70,9 +70,10 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_kernel(FwdArgs a) {
   }
 
   const KeyRanges kr = train_key_ranges(q0, kBM, a.n, a.bs, kTileRows);
-  const int n_first = kr.t1 - kr.t0;
-  const int n_tiles = n_first + (kr.t3 - kr.t2);
-  auto tile_of = [&](int i) { return i < n_first ? kr.t0 + i : kr.t2 + (i - n_first); };
+  const int t0 = wave_uniform(kr.t0), t2 = wave_uniform(kr.t2);
+  const int n_first = wave_uniform(kr.t1 - kr.t0);
+  const int n_tiles = n_first + wave_uniform(kr.t3 - kr.t2);
+  auto tile_of = [&](int i) { return i < n_first ? t0 + i : t2 + (i - n_first); };
 
   TileStager<kThreads, 2> st;
   {
@@ -95,7 +96,10 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_kernel(FwdArgs a) {
     lsum[qb] = 0.f;
   }
 
-  if (n_tiles > 0) {
+  // Every row group sees at least its own block, so n_tiles >= 1 and the
+  // prologue is unconditional (keeping it on every path also leaves no load
+  // pending into the loop).
+  {
     stage_load(0);
     __bf16* dst[2] = {smem[0][0], smem[0][1]};
     st.store(dst);
@@ -105,7 +109,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_kernel(FwdArgs a) {
   for (int it = 0; it < n_tiles; ++it) {
     const int stage = it & 1;
     if (it + 1 < n_tiles) stage_load(it + 1);
-    const int k0 = tile_of(it) * kTileRows;
+    const int k0 = wave_uniform(tile_of(it) * kTileRows);
     const __bf16* ks = smem[stage][0];
     const __bf16* vs = smem[stage][1];
 
@@ -115,7 +119,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_kernel(FwdArgs a) {
     for (int qb = 0; qb < RB; ++qb)
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb) {
-        cls[qb][sb] = train_class(qrow0 + 32 * qb, 32, k0 + 32 * sb, 32, a.n, a.bs);
+        cls[qb][sb] = wave_uniform(train_class(qrow0 + 32 * qb, 32, k0 + 32 * sb, 32, a.n, a.bs));
         live[sb] |= cls[qb][sb];
       }
 

@@ -92,6 +92,18 @@ __device__ __forceinline__ float shfl_xor(float x, int m) {
   return __shfl_xor(x, m, 64);
 }
 
+// A value the program knows to be the same in every lane of the wave (the
+// wave index, tile counts derived from blockIdx): moving it to an SGPR lets
+// the compiler branch on it with scalar branches instead of exec masks.
+__device__ __forceinline__ int wave_uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// Waits for every outstanding vector-memory load of this wave. Placed after
+// the prologue loads so that no load is still pending on any path into a
+// main loop; otherwise the compiler's conservative wait-count merge at the
+// loop header makes the first use of prologue registers wait on the loop's
+// own prefetch loads.
+__device__ __forceinline__ void wait_all_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 // 16-byte global load/store helpers (bf16 rows are 128 B at head_dim 64).
 __device__ __forceinline__ u32x4 ld16(const void* p) {
   return *reinterpret_cast<const u32x4*>(p);

@@ -45,7 +45,7 @@ __global__ __launch_bounds__(kThreads) void decode_partial(DecodeArgs a) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = wave_uniform(tid >> 6);
   const int l32 = lane & 31;
   const int g = lane >> 5;
 
