@@ -37,11 +37,14 @@ _flush_buf: Tensor | None = None
 
 
 def flush_caches() -> None:
-    """Evict L2 and the Infinity Cache by zeroing a 1 GiB buffer."""
+    """Evict L2 and the Infinity Cache by reading a 1 GiB buffer. A read
+    leaves the caches holding clean lines; zeroing the buffer (the
+    reference's method) would leave up to the cache capacity of dirty lines
+    whose write-back then competes with the timed kernel for HBM."""
     global _flush_buf
     if _flush_buf is None:
-        _flush_buf = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device="cuda")
-    _flush_buf.zero_()
+        _flush_buf = torch.zeros(FLUSH_BYTES // 4, dtype=torch.int32, device="cuda")
+    _flush_buf.max()
 
 
 def bench(fn: Callable[[], Any], warmup: int = 25, rep: int = 100, flush: bool = True) -> Timing:
