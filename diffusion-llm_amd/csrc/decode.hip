@@ -15,8 +15,14 @@
 //   operand: a 128-byte key row is covered by 8 consecutive lanes' loads);
 //   V goes through a wave-private row-major LDS tile and is read transposed
 //   (ds_read_b64_tr_b16) as the A operand of O^T += V^T P^T.
+// decode16_partial: the same for q_len <= 16 (a cached denoising step of one
+//   16-token block) on v_mfma_f32_16x16x32_bf16, so no MFMA row or softmax
+//   lane is spent on absent queries. Each wave double-buffers its 64-key K/V
+//   chunks in registers: the loads of chunk i+1 are in flight while chunk i is
+//   computed.
 // decode_combine: merges the splits, weights exp2(lse_s - max lse) (the
-//   reference's split_kv_reduce_kern arithmetic, :109-127).
+//   reference's split_kv_reduce_kern arithmetic, :109-127), 4 outputs per
+//   thread.
 #include "bd3_device.h"
 #include "bd3_launch.h"
 #include "bd3_mask.h"
@@ -119,7 +125,7 @@ __global__ __launch_bounds__(kThreads) void decode_partial(DecodeArgs a) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int key = j0 + 8 * (r >> 2) + 4 * g + (r & 3);
-            if (key >= khi || key >= hi) s[sb][r] = -INFINITY;
+            s[sb][r] = (key < khi && key < hi) ? s[sb][r] : -INFINITY;
           }
         }
       } else {
@@ -218,6 +224,214 @@ __global__ __launch_bounds__(kThreads) void decode_partial(DecodeArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// q_len <= 16: 16-row query tile on v_mfma_f32_16x16x32_bf16.
+//   S^T block (16 keys x 16 rows) = K Q^T: A = K (lane: key 16kb + lane%16,
+//   d 32c + 8h .. +7 with h = lane/16), B = Q^T (lane: row lane%16, same d);
+//   result lane (row lane%16, h) holds keys 16kb + 4h + r.
+//   O^T (16 d x 16 rows) += V^T P^T over 32 keys: B = P^T from the S^T
+//   registers of key blocks 2t and 2t+1, A = V^T read transposed from the
+//   wave's row-major LDS tile with the same key order.
+constexpr int kQ16 = 16;
+
+struct Merge16 {
+  float o[kNW][kHeadDim][kQ16 + 1];
+  float m[kNW][kQ16];
+  float l[kNW][kQ16];
+};
+constexpr size_t kSmem16 = kVBytes > sizeof(Merge16) ? kVBytes : sizeof(Merge16);
+constexpr float kRescale16 = 8.0f;
+
+struct Chunk16 {
+  u32x4 k[4][2];  // K A-operands [16-key block][32-d chunk]
+  u32x4 v[8];     // V rows: lane + 64j -> row (lane + 64j)/8, 16-byte part lane%8
+};
+
+#ifndef BD3_DEC16_DBUF
+#define BD3_DEC16_DBUF 0
+#endif
+#ifndef BD3_DEC16_OCC
+#define BD3_DEC16_OCC 4
+#endif
+
+__global__ __launch_bounds__(kThreads, BD3_DEC16_OCC) void decode16_partial(DecodeArgs a) {
+  __shared__ __attribute__((aligned(16))) char smem[kSmem16];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = wave_uniform(tid >> 6);
+  const int l16 = lane & 15;
+  const int hq = lane >> 4;  // 16-lane group
+  __bf16* vs = reinterpret_cast<__bf16*>(smem) + wave * kVElems;
+
+  const int split = blockIdx.x;
+  const int bh = blockIdx.z;
+  const int b = bh / a.heads, h = bh - b * a.heads;
+  const uint16_t* qp = a.q + b * a.sq.b + h * a.sq.h;
+  const uint16_t* kp = a.k + b * a.sk.b + h * a.sk.h;
+  const uint16_t* vp = a.v + b * a.sv.b + h * a.sv.h;
+
+  const int qrow = imin(l16, a.q_len - 1);
+  bf16x8 qreg[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+    qreg[c] = __builtin_bit_cast(bf16x8, ld16(qp + (int64_t)qrow * a.sq.s + 32 * c + 8 * hq));
+  // Row l16 sees keys [0, khi); rows past q_len are computed and dropped.
+  const int pos = a.kv_len - a.q_len + l16;
+  const int khi = l16 < a.q_len ? imin((pos / a.bs + 1) * a.bs, a.kv_len) : a.kv_len;
+
+  const int key_end = wave_uniform(decode_key_end(0, kQ16, a.q_len, a.kv_len, a.bs));
+  const int lo = wave_uniform(split * a.split_len);
+  const int hi = wave_uniform(imin(lo + a.split_len, key_end));
+  const int n_chunks = hi > lo ? (hi - lo + kChunk - 1) / kChunk : 0;
+  // keys below kfull are seen by every row (row 0 has the smallest position)
+  const int kfull = wave_uniform(imin(((a.kv_len - a.q_len) / a.bs + 1) * a.bs, a.kv_len));
+
+  auto load = [&](Chunk16& cb, int ch) {
+    const int c0 = lo + ch * kChunk;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const int key = imin(c0 + 16 * kb + l16, a.kv_len - 1);
+#pragma unroll
+      for (int c = 0; c < 2; ++c) cb.k[kb][c] = ld16(kp + (int64_t)key * a.sk.s + 32 * c + 8 * hq);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int key = imin(c0 + (lane >> 3) + 8 * j, a.kv_len - 1);
+      cb.v[j] = ld16(vp + (int64_t)key * a.sv.s + 8 * (lane & 7));
+    }
+  };
+
+  f32x4 o[4] = {};  // O^T [16-d block]: lane (row l16, hq) holds d 16db + 4hq + r
+  float m = -INFINITY, lsum = 0.f;
+
+  auto compute = [&](const Chunk16& cb, int ch) {
+    const int c0 = lo + ch * kChunk;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      *reinterpret_cast<u32x4*>(&vs[((lane >> 3) + 8 * j) * kStride + 8 * (lane & 7)]) = cb.v[j];
+    f32x4 s[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      s[kb] = mfma16(__builtin_bit_cast(bf16x8, cb.k[kb][0]), qreg[0], f32x4{});
+      s[kb] = mfma16(__builtin_bit_cast(bf16x8, cb.k[kb][1]), qreg[1], s[kb]);
+    }
+    if (c0 + kChunk > kfull || c0 + kChunk > hi) {  // partial chunk (uniform)
+      const int lim = imin(khi, hi);
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          s[kb][r] = (c0 + 16 * kb + 4 * hq + r < lim) ? s[kb][r] : -INFINITY;
+    }
+    float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
+                     fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
+    mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(s[2][0], s[2][1]), fmaxf(s[2][2], s[2][3])),
+                         fmaxf(fmaxf(s[3][0], s[3][1]), fmaxf(s[3][2], s[3][3]))));
+    mx = fmaxf(mx, shfl_xor(mx, 16));
+    mx = max_xor32(mx);
+    const float mt = mx * a.scale_log2;
+    if (__ballot(mt > m + kRescale16) != 0) {
+      const float mn = fmaxf(m, mt);
+      const float alpha = (mn == -INFINITY) ? 1.f : fast_exp2(m - mn);
+      m = mn;
+      lsum *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) o[db] *= alpha;
+    }
+    const float mu = (m == -INFINITY) ? 0.f : m;
+    float p[4][4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        p[kb][r] = fast_exp2(fmaf(s[kb][r], a.scale_log2, -mu));
+        lsum += p[kb][r];
+      }
+    const int tr_row = l16 >> 2;
+    const int tr_col = 4 * (lane & 3);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const bf16x8 pop = to_bf16x8(p[2 * t][0], p[2 * t][1], p[2 * t][2], p[2 * t][3],
+                                   p[2 * t + 1][0], p[2 * t + 1][1], p[2 * t + 1][2], p[2 * t + 1][3]);
+      const int row = 32 * t + 4 * hq + tr_row;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const bf16x8 va = cat8(lds_read_tr(&vs[row * kStride + 16 * db + tr_col]),
+                               lds_read_tr(&vs[(row + 16) * kStride + 16 * db + tr_col]));
+        o[db] = mfma16(va, pop, o[db]);
+      }
+    }
+  };
+
+#if BD3_DEC16_DBUF
+  // Register double buffering: chunk i+1 (this wave's next) loads while chunk i computes.
+  Chunk16 ca, cb;
+  int ch = wave;
+  if (ch < n_chunks) load(ca, ch);
+  while (ch < n_chunks) {
+    const int nx = ch + kNW;
+    if (nx < n_chunks) load(cb, nx);
+    compute(ca, ch);
+    ch = nx;
+    if (ch >= n_chunks) break;
+    const int nx2 = ch + kNW;
+    if (nx2 < n_chunks) load(ca, nx2);
+    compute(cb, ch);
+    ch = nx2;
+  }
+#else
+  for (int ch = wave; ch < n_chunks; ch += kNW) {
+    Chunk16 ca;
+    load(ca, ch);
+    compute(ca, ch);
+  }
+#endif
+
+  // Merge the four waves' states.
+  lsum += shfl_xor(lsum, 16);
+  lsum = sum_xor32(lsum);
+  __syncthreads();  // V staging area is reused below
+  Merge16* ml = reinterpret_cast<Merge16*>(smem);
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ml->o[wave][16 * db + 4 * hq + r][l16] = o[db][r];
+  if (hq == 0) {
+    ml->m[wave][l16] = m;
+    ml->l[wave][l16] = lsum;
+  }
+  __syncthreads();
+
+  // 256 threads x 4 outputs = 16 rows x 64 d.
+  const int row = tid >> 4, d0 = 4 * (tid & 15);
+  float mm = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kNW; ++w) mm = fmaxf(mm, ml->m[w][row]);
+  const float mu = (mm == -INFINITY) ? 0.f : mm;
+  float lt = 0.f;
+  f32x4 ot = {};
+#pragma unroll
+  for (int w = 0; w < kNW; ++w) {
+    const float wgt = fast_exp2(ml->m[w][row] - mu);
+    lt += wgt * ml->l[w][row];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ot[j] += wgt * ml->o[w][d0 + j][row];
+  }
+  if (a.n_splits == 1) {
+    if (row < a.q_len) {
+      const float inv = 1.f / lt;
+      *reinterpret_cast<bf16x4*>(a.o + b * a.so.b + h * a.so.h + (int64_t)row * a.so.s + d0) =
+          to_bf16x4(ot[0] * inv, ot[1] * inv, ot[2] * inv, ot[3] * inv);
+    }
+  } else {
+    const int64_t slot = (int64_t)bh * a.q_tiles * a.n_splits + split;  // q_tiles == 1
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    *reinterpret_cast<f32x4*>(&a.part_o[(slot * kQT + row) * kHeadDim + d0]) = ot * inv;
+    if ((tid & 15) == 0) a.part_lse[slot * kQT + row] = lt > 0.f ? mm + fast_log2(lt) : -INFINITY;
+  }
+}
+
+// Split merge: thread -> (row, 4 consecutive d); rows in passes of 16.
 __global__ __launch_bounds__(kThreads) void decode_combine(DecodeArgs a) {
   const int qt = blockIdx.x;
   const int bh = blockIdx.y;
@@ -225,22 +439,23 @@ __global__ __launch_bounds__(kThreads) void decode_combine(DecodeArgs a) {
   const int i0 = qt * kQT;
   uint16_t* op = a.o + b * a.so.b + h * a.so.h;
   const int64_t slot0 = ((int64_t)bh * a.q_tiles + qt) * a.n_splits;
+  const int d0 = 4 * (threadIdx.x & 15);
 #pragma unroll
-  for (int j = 0; j < (kQT * kHeadDim) / kThreads; ++j) {
-    const int e = threadIdx.x + kThreads * j;
-    const int row = e >> 6, d = e & 63;
+  for (int pass = 0; pass < kQT / 16; ++pass) {
+    const int row = pass * 16 + (threadIdx.x >> 4);
     if (i0 + row >= a.q_len) continue;
     float mm = -INFINITY;
     for (int s = 0; s < a.n_splits; ++s) mm = fmaxf(mm, a.part_lse[(slot0 + s) * kQT + row]);
-    float wt = 0.f, acc = 0.f;
+    float wt = 0.f;
+    f32x4 acc = {};
     for (int s = 0; s < a.n_splits; ++s) {
-      const float lse = a.part_lse[(slot0 + s) * kQT + row];
-      const float w = fast_exp2(lse - mm);  // -inf lse (empty split) -> 0
+      const float w = fast_exp2(a.part_lse[(slot0 + s) * kQT + row] - mm);  // empty split -> 0
       wt += w;
-      acc += w * a.part_o[((slot0 + s) * kQT + row) * kHeadDim + d];
+      acc += w * *reinterpret_cast<const f32x4*>(&a.part_o[((slot0 + s) * kQT + row) * kHeadDim + d0]);
     }
-    const __bf16 y = (__bf16)(acc / wt);
-    op[(int64_t)(i0 + row) * a.so.s + d] = __builtin_bit_cast(uint16_t, y);
+    const float inv = 1.f / wt;
+    *reinterpret_cast<bf16x4*>(op + (int64_t)(i0 + row) * a.so.s + d0) =
+        to_bf16x4(acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv);
   }
 }
 
@@ -262,7 +477,10 @@ __global__ void mask_dump_kernel(uint8_t* out, int mode, int rows, int cols, int
 
 hipError_t launch_decode(const DecodeArgs& a, int /*qt*/, hipStream_t stream) {
   dim3 grid(a.n_splits, a.q_tiles, a.bh);
-  hipLaunchKernelGGL(decode_partial, grid, dim3(kThreads), 0, stream, a);
+  if (a.q_len <= kQ16)
+    hipLaunchKernelGGL(decode16_partial, grid, dim3(kThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL(decode_partial, grid, dim3(kThreads), 0, stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.n_splits == 1) return e;
   hipLaunchKernelGGL(decode_combine, dim3(a.q_tiles, a.bh), dim3(kThreads), 0, stream, a);
