@@ -59,11 +59,13 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_bwd_dq_kernel(BwdArgs a) {
   const int qrow0 = q0 + 32 * RB * wave;
   bf16x8 qreg[RB][4], doreg[RB][4];
   RowIntervals riv[RB];
+  RowGroup rgs[RB];
   float lrow[RB], drow[RB];
 #pragma unroll
   for (int qb = 0; qb < RB; ++qb) {
     const int myq = qrow0 + 32 * qb + l32;
     riv[qb] = train_row_intervals(myq, a.n, a.bs);
+    rgs[qb] = uniform_row_group(qrow0 + 32 * qb, 32, a.n, a.bs);
     float dsum = 0.f;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -121,7 +123,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_bwd_dq_kernel(BwdArgs a) {
     for (int qb = 0; qb < RB; ++qb)
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb) {
-        cls[qb][sb] = wave_uniform(train_class(qrow0 + 32 * qb, 32, k0 + 32 * sb, 32, a.n, a.bs));
+        cls[qb][sb] = row_group_class(rgs[qb], k0 + 32 * sb, 32, a.n);
         live[sb] |= cls[qb][sb];
       }
 
@@ -229,10 +231,12 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_bwd_dkdv_kernel(BwdArgs a) 
   const int kw = k0 + 32 * KB * wave;
   bf16x8 kreg[KB][4], vreg[KB][4];
   RowIntervals civ[KB];
+  KeyGroup kgs[KB];
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb) {
     const int key = kw + 32 * kb + l32;
     civ[kb] = train_col_intervals(key, a.n, a.bs);
+    kgs[kb] = uniform_key_group(kw + 32 * kb, 32, a.n, a.bs);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       kreg[kb][c] = __builtin_bit_cast(bf16x8, ld16(kp + (int64_t)key * a.sk.s + 16 * c + 8 * g));
@@ -292,7 +296,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_bwd_dkdv_kernel(BwdArgs a) 
     for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
-        cls[qb][kb] = wave_uniform(train_class(q0 + 32 * qb, 32, kw + 32 * kb, 32, a.n, a.bs));
+        cls[qb][kb] = key_group_class(kgs[kb], q0 + 32 * qb, 32, a.n);
         live[qb] |= cls[qb][kb];
       }
 

@@ -60,10 +60,12 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_kernel(FwdArgs a) {
   const int qrow0 = q0 + 32 * RB * wave;
   bf16x8 qreg[RB][4];
   RowIntervals riv[RB];
+  RowGroup rgs[RB];
 #pragma unroll
   for (int qb = 0; qb < RB; ++qb) {
     const int myq = qrow0 + 32 * qb + l32;
     riv[qb] = train_row_intervals(myq, a.n, a.bs);
+    rgs[qb] = uniform_row_group(qrow0 + 32 * qb, 32, a.n, a.bs);
 #pragma unroll
     for (int c = 0; c < 4; ++c)
       qreg[qb][c] = __builtin_bit_cast(bf16x8, ld16(qp + (int64_t)myq * a.sq.s + 16 * c + 8 * g));
@@ -119,7 +121,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_kernel(FwdArgs a) {
     for (int qb = 0; qb < RB; ++qb)
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb) {
-        cls[qb][sb] = wave_uniform(train_class(qrow0 + 32 * qb, 32, k0 + 32 * sb, 32, a.n, a.bs));
+        cls[qb][sb] = row_group_class(rgs[qb], k0 + 32 * sb, 32, a.n);
         live[sb] |= cls[qb][sb];
       }
 
@@ -176,14 +178,13 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_kernel(FwdArgs a) {
           if (cls[qb][sb] == kNone) continue;
           float p[16];
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            p[r] = fast_exp2(fmaf(s[qb][sb][r], a.scale_log2, -mu));
-            lsum[qb] += p[r];
-          }
+          for (int r = 0; r < 16; ++r) p[r] = fast_exp2(fmaf(s[qb][sb][r], a.scale_log2, -mu));
 #pragma unroll
-          for (int kc = 0; kc < 2; ++kc)
+          for (int kc = 0; kc < 2; ++kc) {
             pop[qb][sb][kc] = to_bf16x8(p[8 * kc], p[8 * kc + 1], p[8 * kc + 2], p[8 * kc + 3],
                                         p[8 * kc + 4], p[8 * kc + 5], p[8 * kc + 6], p[8 * kc + 7]);
+            lsum[qb] = sum_bf16x8(pop[qb][sb][kc], lsum[qb]);
+          }
         }
       }
 
@@ -230,8 +231,194 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_kernel(FwdArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Software-pipelined forward, one 32-row block per wave. Iteration i issues
+// the S^T MFMAs of key tile i+1 before the softmax and PV of tile i, so the
+// matrix cores work while the VALU runs the softmax; tile i+2 is meanwhile
+// loaded into registers. LDS holds two tiles: K of a stage is consumed one
+// iteration before its V, so a stage is refilled (between two barriers) right
+// after the PV that reads its V. Each tile is classified for the wave as dead
+// (skipped), full (no mask) or masked (interval mask, which also zeroes a dead
+// 32-key half), so each path is straight-line code.
+enum WaveTile { kTileDead = 0, kTileFull = 1, kTileMasked = 2 };
+
+template <int NW, int OCC>
+__global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_pipe_kernel(FwdArgs a) {
+  constexpr int kThreads = NW * 64;
+  constexpr int kBM = 32 * NW;
+  __shared__ __attribute__((aligned(16))) __bf16 smem[2][2][kTileElems];  // [stage][K|V]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = wave_uniform(tid >> 6);
+  const int l32 = lane & 31;
+  const int g = lane >> 5;
+
+  const BlockOrder bo(a.bh, a.heads);
+  const int tiles_half = a.n / kBM;
+  const int t = tiles_half - 1 - (bo.rank >> 1);
+  const int q0 = ((bo.rank & 1) ? 0 : a.n) + t * kBM;
+
+  const uint16_t* qp = a.q + bo.b * a.sq.b + bo.h * a.sq.h;
+  const uint16_t* kp = a.k + bo.b * a.sk.b + bo.h * a.sk.h;
+  const uint16_t* vp = a.v + bo.b * a.sv.b + bo.h * a.sv.h;
+
+  const int qrow0 = q0 + 32 * wave;
+  const int myq = qrow0 + l32;
+  const RowIntervals riv = train_row_intervals(myq, a.n, a.bs);
+  const RowGroup rg = uniform_row_group(qrow0, 32, a.n, a.bs);
+  bf16x8 qreg[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    qreg[c] = __builtin_bit_cast(bf16x8, ld16(qp + (int64_t)myq * a.sq.s + 16 * c + 8 * g));
+
+  const KeyRanges kr = train_key_ranges(q0, kBM, a.n, a.bs, kTileRows);
+  const int t0 = wave_uniform(kr.t0), t2 = wave_uniform(kr.t2);
+  const int n_first = wave_uniform(kr.t1 - kr.t0);
+  const int n_tiles = n_first + wave_uniform(kr.t3 - kr.t2);
+  auto tile_of = [&](int i) { return i < n_first ? t0 + i : t2 + (i - n_first); };
+
+  TileStager<kThreads, 2> st;
+  {
+    const int64_t rs[2] = {a.sk.s, a.sv.s};
+    st.init(tid, rs);
+  }
+  auto stage_load = [&](int i) {
+    const int64_t k0 = (int64_t)tile_of(i) * kTileRows;
+    const uint16_t* base[2] = {kp + k0 * a.sk.s, vp + k0 * a.sv.s};
+    st.load(base);
+  };
+  auto stage_store = [&](int stage) {
+    __bf16* dst[2] = {smem[stage][0], smem[stage][1]};
+    st.store(dst);
+  };
+  auto tclass = [&](int i) {
+    const int k0 = wave_uniform(tile_of(i) * kTileRows);
+    const int c0 = row_group_class(rg, k0, 32, a.n);
+    const int c1 = row_group_class(rg, k0 + 32, 32, a.n);
+    const int r = (c0 | c1) == kNone ? kTileDead
+                                     : ((c0 == kFull && c1 == kFull) ? kTileFull : kTileMasked);
+    return wave_uniform(r);
+  };
+  auto mma_s = [&](const __bf16* ks, f32x16& s0, f32x16& s1) {
+    s0 = f32x16{};
+    s1 = f32x16{};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const bf16x8 k0op = lds_row_op(ks, 0, c, lane);
+      const bf16x8 k1op = lds_row_op(ks, 32, c, lane);
+      s0 = mfma32(k0op, qreg[c], s0);
+      s1 = mfma32(k1op, qreg[c], s1);
+    }
+  };
+
+  f32x16 o[2] = {};  // O^T [d block]
+  float m = -INFINITY, lsum = 0.f;
+
+  auto soft_pv = [&](int i, int cls, f32x16& s0, f32x16& s1, const __bf16* vs) {
+    if (cls == kTileMasked) {
+      const int k0 = tile_of(i) * kTileRows;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = k0 + 8 * (r >> 2) + 4 * g + (r & 3);
+        s0[r] = iv_has(riv, key) ? s0[r] : -INFINITY;
+        s1[r] = iv_has(riv, key + 32) ? s1[r] : -INFINITY;
+      }
+    }
+    float mx = fmaxf(s0[0], s1[0]);
+#pragma unroll
+    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
+    const float mt = max_xor32(mx) * a.scale_log2;
+    if (__ballot(mt > m + kRescale) != 0) {
+      const float mn = fmaxf(m, mt);
+      const float alpha = (mn == -INFINITY) ? 1.f : fast_exp2(m - mn);
+      m = mn;
+      lsum *= alpha;
+      o[0] *= alpha;
+      o[1] *= alpha;
+    }
+    const float mu = (m == -INFINITY) ? 0.f : m;
+    float p0[16], p1[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      p0[r] = fast_exp2(fmaf(s0[r], a.scale_log2, -mu));
+      p1[r] = fast_exp2(fmaf(s1[r], a.scale_log2, -mu));
+    }
+    bf16x8 pop[2][2];
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc) {
+      pop[0][kc] = to_bf16x8(p0[8 * kc], p0[8 * kc + 1], p0[8 * kc + 2], p0[8 * kc + 3],
+                             p0[8 * kc + 4], p0[8 * kc + 5], p0[8 * kc + 6], p0[8 * kc + 7]);
+      pop[1][kc] = to_bf16x8(p1[8 * kc], p1[8 * kc + 1], p1[8 * kc + 2], p1[8 * kc + 3],
+                             p1[8 * kc + 4], p1[8 * kc + 5], p1[8 * kc + 6], p1[8 * kc + 7]);
+      lsum = sum_bf16x8(pop[0][kc], lsum);
+      lsum = sum_bf16x8(pop[1][kc], lsum);
+    }
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+          o[db] = mfma32(lds_tr_op(vs, 32 * sb + 16 * kc, 32 * db, lane), pop[sb][kc], o[db]);
+  };
+
+  // Prologue: tiles 0 and 1 into the two stages, S^T of tile 0.
+  stage_load(0);
+  stage_store(0);
+  if (n_tiles > 1) {
+    stage_load(1);
+    stage_store(1);
+  }
+  __syncthreads();
+  f32x16 sa0, sa1, sb0, sb1;
+  int ca = tclass(0), cb = kTileDead;
+  if (ca != kTileDead) mma_s(smem[0][0], sa0, sa1);
+
+  // One pipeline step: S^T of tile it+1, softmax + PV of tile it, refill.
+  auto step = [&](int it, int cur, f32x16& c0, f32x16& c1, int& nxt, f32x16& n0, f32x16& n1) {
+    const int stage = it & 1;
+    const bool refill = it + 2 < n_tiles;
+    if (refill) stage_load(it + 2);
+    nxt = kTileDead;
+    if (it + 1 < n_tiles) {
+      nxt = tclass(it + 1);
+      if (nxt != kTileDead) mma_s(smem[stage ^ 1][0], n0, n1);
+    }
+    if (cur != kTileDead) soft_pv(it, cur, c0, c1, smem[stage][1]);
+    if (refill) {
+      __syncthreads();  // every wave is done with this stage's V
+      stage_store(stage);
+    }
+    __syncthreads();
+  };
+  for (int it = 0; it < n_tiles; it += 2) {
+    step(it, ca, sa0, sa1, cb, sb0, sb1);
+    if (it + 1 >= n_tiles) break;
+    step(it + 1, cb, sb0, sb1, ca, sa0, sa1);
+  }
+
+  const float ltot = sum_xor32(lsum);
+  const float inv = 1.f / ltot;
+  uint16_t* op = a.o + bo.b * a.so.b + bo.h * a.so.h + (int64_t)myq * a.so.s;
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg)
+      *reinterpret_cast<bf16x4*>(op + 32 * db + 8 * rg + 4 * g) =
+          to_bf16x4(o[db][4 * rg] * inv, o[db][4 * rg + 1] * inv, o[db][4 * rg + 2] * inv,
+                    o[db][4 * rg + 3] * inv);
+  if (g == 0) a.lse[(int64_t)bo.bh * 2 * a.n + myq] = (m + fast_log2(ltot)) * kLn2;
+}
+
 }  // namespace
 
+#ifndef BD3_FWD_PIPE
+#define BD3_FWD_PIPE 0
+#endif
+#ifndef BD3_FWD_PIPE_OCC
+#define BD3_FWD_PIPE_OCC 2
+#endif
 #ifndef BD3_FWD_NW
 #define BD3_FWD_NW 4
 #endif
@@ -246,7 +433,10 @@ hipError_t launch_attn_fwd(const FwdArgs& a, hipStream_t stream) {
   constexpr int kNW = BD3_FWD_NW, kRB = BD3_FWD_RB, kOcc = BD3_FWD_OCC;
   constexpr int kBM = 32 * kNW * kRB;
   static_assert(128 % kBM == 0 || kBM % 128 == 0, "tile must align with n % 128 == 0");
-  if (a.n % kBM == 0) {
+  if (BD3_FWD_PIPE && a.n % (32 * kNW) == 0) {
+    hipLaunchKernelGGL((attn_fwd_pipe_kernel<kNW, BD3_FWD_PIPE_OCC>), dim3(a.bh * (2 * a.n / (32 * kNW))),
+                       dim3(kNW * 64), 0, stream, a);
+  } else if (a.n % kBM == 0) {
     hipLaunchKernelGGL((attn_fwd_kernel<kNW, kRB, kOcc>), dim3(a.bh * (2 * a.n / kBM)), dim3(kNW * 64), 0,
                        stream, a);
   } else {  // n % 128 == 0 always holds (validated): 4 waves x 32 rows

@@ -113,30 +113,101 @@ enum TileClass { kNone = 0, kFull = 1, kPartial = 2 };
 // training mask. Rows must lie in one half and keys in one half (true for
 // 32-aligned groups when n % 32 == 0). kNone and kFull are exact; kPartial
 // means some but not all pairs are live.
-BD3_HD int train_class(int q0, int R, int k0, int C, int n, int bs) {
-  const bool qc = q0 >= n, kc = k0 >= n;
-  const int r0 = qc ? q0 - n : q0;
-  const int r1 = r0 + R - 1;
-  const int b0 = r0 / bs, b1 = r1 / bs;
+//
+// A kernel that classifies many key groups against one fixed row group
+// precomputes the row group's bounds once (RowGroup: no division per tile);
+// a kernel with a fixed key group classifies row groups with KeyGroup.
+struct RowGroup {
+  int clean;      // rows in the clean half
+  int diag_lo;    // noisy rows: keys [diag_lo, diag_hi) hold their own blocks
+  int diag_hi;
+  int one_block;  // noisy rows all in one block
+  int full_end;   // clean-key offsets [0, full_end) are seen by every row
+  int live_end;   // clean-key offsets >= live_end are seen by no row
+};
+
+BD3_HD RowGroup train_row_group(int q0, int R, int n, int bs) {
+  RowGroup g;
+  g.clean = q0 >= n;
+  const int r0 = g.clean ? q0 - n : q0;
+  const int b0 = r0 / bs, b1 = (r0 + R - 1) / bs;
+  g.diag_lo = bs * b0;
+  g.diag_hi = imin(bs * (b1 + 1), n);
+  g.one_block = b0 == b1;
+  if (g.clean) {  // row in block b sees clean keys [0, min(bs*(b+1), n))
+    g.full_end = imin(bs * (b0 + 1), n);
+    g.live_end = imin(bs * (b1 + 1), n);
+  } else {        // row in block b sees clean keys [0, bs*b)
+    g.full_end = bs * b0;
+    g.live_end = bs * b1;
+  }
+  return g;
+}
+
+BD3_HD int row_group_class(const RowGroup& g, int k0, int C, int n) {
+  const bool kc = k0 >= n;
   const int a = kc ? k0 - n : k0;  // key offset inside its half
   const int e = a + C;
-  if (!qc && !kc) {  // block diagonal
-    const int lo = bs * b0, hi = imin(bs * (b1 + 1), n);
-    if (e <= lo || a >= hi) return kNone;
-    if (b0 == b1 && lo <= a && e <= hi) return kFull;
+  if (!kc) {
+    if (g.clean) return kNone;  // clean rows never see noisy keys
+    if (e <= g.diag_lo || a >= g.diag_hi) return kNone;
+    if (g.one_block && g.diag_lo <= a && e <= g.diag_hi) return kFull;
     return kPartial;
   }
-  if (!qc && kc) {  // row in block b sees clean keys [0, bs*b)
-    if (a >= bs * b1) return kNone;
-    if (e <= bs * b0) return kFull;
+  if (a >= g.live_end) return kNone;
+  if (e <= g.full_end) return kFull;
+  return kPartial;
+}
+
+BD3_HD int train_class(int q0, int R, int k0, int C, int n, int bs) {
+  return row_group_class(train_row_group(q0, R, n, bs), k0, C, n);
+}
+
+// The transpose: a fixed key group [k0, k0+C) classified against row groups.
+struct KeyGroup {
+  int clean;        // keys in the clean half
+  int noisy_lo;     // noisy keys: noisy rows [noisy_lo, noisy_hi) hold their blocks
+  int noisy_hi;
+  int one_block;    // keys all in one block
+  int nz_live_lo;   // clean keys: noisy rows >= nz_live_lo see some key,
+  int nz_full_lo;   //   noisy rows >= nz_full_lo see every key (row offsets)
+  int cl_live_lo;   //   clean row offsets >= cl_live_lo see some key,
+  int cl_full_lo;   //   clean row offsets >= cl_full_lo see every key
+};
+
+BD3_HD KeyGroup train_key_group(int k0, int C, int n, int bs) {
+  KeyGroup g;
+  g.clean = k0 >= n;
+  const int a0 = g.clean ? k0 - n : k0;
+  const int kb0 = a0 / bs, kb1 = (a0 + C - 1) / bs;
+  g.noisy_lo = bs * kb0;
+  g.noisy_hi = imin(bs * (kb1 + 1), n);
+  g.one_block = kb0 == kb1;
+  // noisy row of block b sees clean key block kb iff b > kb
+  g.nz_live_lo = imin(bs * (kb0 + 1), n);
+  g.nz_full_lo = imin(bs * (kb1 + 1), n);
+  // clean row of block b sees clean key block kb iff b >= kb
+  g.cl_live_lo = bs * kb0;
+  g.cl_full_lo = bs * kb1;
+  return g;
+}
+
+BD3_HD int key_group_class(const KeyGroup& g, int q0, int R, int n) {
+  const bool qc = q0 >= n;
+  const int r = qc ? q0 - n : q0;  // row offset inside its half
+  const int e = r + R;
+  if (!g.clean) {
+    if (qc) return kNone;  // clean rows never see noisy keys
+    if (e <= g.noisy_lo || r >= g.noisy_hi) return kNone;
+    if (g.one_block && g.noisy_lo <= r && e <= g.noisy_hi) return kFull;
     return kPartial;
   }
-  if (qc && kc) {  // row in block b sees clean keys [0, min(bs*(b+1), n))
-    if (a >= imin(bs * (b1 + 1), n)) return kNone;
-    if (e <= imin(bs * (b0 + 1), n)) return kFull;
-    return kPartial;
-  }
-  return kNone;  // clean rows never see noisy keys
+  const int live_lo = qc ? g.cl_live_lo : g.nz_live_lo;
+  const int full_lo = qc ? g.cl_full_lo : g.nz_full_lo;
+  const int row_end = qc ? e : imin(e, n);
+  if (row_end <= live_lo || (!qc && r >= n)) return kNone;
+  if (r >= full_lo) return kFull;
+  return kPartial;
 }
 
 // Key ranges (in key-tile units of `tile` keys) a training row group

@@ -66,6 +66,44 @@ __device__ __forceinline__ bf16x8 lds_tr_op(const __bf16* tile, int r0, int col0
               lds_read_tr(&tile[(row + 8) * kLdsStride + col]));
 }
 
+// Group bounds for tile classification, moved to SGPRs once per wave so
+// each per-tile classification is a few scalar compares.
+__device__ __forceinline__ RowGroup uniform_row_group(int q0, int R, int n, int bs) {
+  RowGroup g = train_row_group(q0, R, n, bs);
+  g.clean = wave_uniform(g.clean);
+  g.diag_lo = wave_uniform(g.diag_lo);
+  g.diag_hi = wave_uniform(g.diag_hi);
+  g.one_block = wave_uniform(g.one_block);
+  g.full_end = wave_uniform(g.full_end);
+  g.live_end = wave_uniform(g.live_end);
+  return g;
+}
+
+__device__ __forceinline__ KeyGroup uniform_key_group(int k0, int C, int n, int bs) {
+  KeyGroup g = train_key_group(k0, C, n, bs);
+  g.clean = wave_uniform(g.clean);
+  g.noisy_lo = wave_uniform(g.noisy_lo);
+  g.noisy_hi = wave_uniform(g.noisy_hi);
+  g.one_block = wave_uniform(g.one_block);
+  g.nz_live_lo = wave_uniform(g.nz_live_lo);
+  g.nz_full_lo = wave_uniform(g.nz_full_lo);
+  g.cl_live_lo = wave_uniform(g.cl_live_lo);
+  g.cl_full_lo = wave_uniform(g.cl_full_lo);
+  return g;
+}
+
+// Sum of the 8 bf16 values of a P operand added to acc, as 4 v_dot2c_f32_bf16
+// against (1, 1): the softmax denominator accumulates exactly the rounded
+// probabilities the PV product uses, at half the VALU cost of fp32 adds.
+__device__ __forceinline__ float sum_bf16x8(bf16x8 v, float acc) {
+  const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 0, 1), one, acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 2, 3), one, acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 4, 5), one, acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 6, 7), one, acc, false);
+  return acc;
+}
+
 // Visibility of key k for a row with intervals iv, as 0/1 without branches.
 __device__ __forceinline__ bool iv_has(const RowIntervals& iv, int k) {
   return ((unsigned)(k - iv.lo1) < (unsigned)(iv.hi1 - iv.lo1)) |

@@ -29,12 +29,19 @@ ARCH = "gfx950"
 # -packed-fp32-ops: hipcc would otherwise fuse float pairs into
 # v_pk_{add,mul,fma}_f32, some forms of which are unreliable on this pool.
 # The host pass warns that it does not know the feature; that is harmless.
+# -mno-amdgpu-ieee -fno-honor-nans: the kernels never produce or consume
+# NaN (masked scores are -inf, every row has a live key), so the IEEE-mode
+# NaN quieting the compiler would otherwise insert before each max (one
+# extra v_max per softmax element) is dropped and max chains fold into
+# v_max3_f32.
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
     "-std=c++17",
     "-fPIC",
     "-munsafe-fp-atomics",
+    "-mno-amdgpu-ieee",
+    "-fno-honor-nans",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-result",
     f"-I{REPO / 'include'}",

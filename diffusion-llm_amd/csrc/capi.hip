@@ -337,6 +337,12 @@ int bd3_train_classify(int32_t n, int32_t block_size, int32_t q0, int32_t k0) {
   return bd3::train_class(q0, 32, k0, 32, n, block_size);
 }
 
+int bd3_train_classify_keys(int32_t n, int32_t block_size, int32_t q0, int32_t k0) {
+  if (n < 32 || n % 32 != 0 || block_size < 1) return -1;
+  if (q0 < 0 || k0 < 0 || q0 + 32 > 2 * n || k0 + 32 > 2 * n || q0 % 32 || k0 % 32) return -1;
+  return bd3::key_group_class(bd3::train_key_group(k0, 32, n, block_size), q0, 32, n);
+}
+
 int bd3_train_intervals(int32_t n, int32_t block_size, int32_t index, int32_t mode, int32_t* out) {
   if (out == nullptr || n < 1 || block_size < 1 || index < 0 || index >= 2 * n) return -1;
   if (mode != 0 && mode != 1) return -1;

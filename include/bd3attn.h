@@ -215,6 +215,13 @@ int bd3_train_tile_census(int32_t n, int32_t block_size, int64_t* out);
 int bd3_train_classify(int32_t n, int32_t block_size, int32_t q0, int32_t k0);
 
 /*
+ * Host-only: the same classification computed the way the key-stationary
+ * backward kernel does it (fixed 32-key group at k0, 32-row group at q0).
+ */
+int bd3_train_classify_keys(int32_t n, int32_t block_size, int32_t q0,
+                            int32_t k0);
+
+/*
  * Host-only: the interval form of the training mask the kernels apply inside
  * partial blocks, for CPU tests. mode 0: the keys row `index` sees; mode 1:
  * the rows that see key `index`. Writes out[0..3] = {lo1, hi1, lo2, hi2}:

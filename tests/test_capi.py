@@ -54,7 +54,8 @@ def test_census_matches_oracle(lib, n, bs):
     assert out[1] == 1024 * (out[2] + out[3])
 
 
-@pytest.mark.parametrize("n,bs", [(64, 1), (64, 16), (96, 7), (128, 32), (128, 128), (160, 64)])
+@pytest.mark.parametrize("n,bs", [(64, 1), (64, 16), (96, 7), (128, 32), (128, 128), (160, 64),
+                                  (256, 256), (192, 48), (64, 100)])
 def test_classification_exact(lib, n, bs):
     """none = no live pair, full = all live, partial = mixed, for every
     (32-row group, 32-key sub-block)."""
@@ -62,9 +63,9 @@ def test_classification_exact(lib, n, bs):
     for q0 in range(0, 2 * n, 32):
         for k0 in range(0, 2 * n, 32):
             blk = m[q0:q0 + 32, k0:k0 + 32]
-            c = lib.bd3_train_classify(n, bs, q0, k0)
             want = 0 if not blk.any() else (1 if blk.all() else 2)
-            assert c == want, (q0, k0)
+            assert lib.bd3_train_classify(n, bs, q0, k0) == want, (q0, k0)
+            assert lib.bd3_train_classify_keys(n, bs, q0, k0) == want, (q0, k0)
 
 
 @pytest.mark.parametrize("n,bs", [(8, 1), (8, 3), (64, 16), (96, 7), (128, 128), (256, 64)])
