@@ -13,7 +13,9 @@ bench/attention_bench.py:89,99, restricted to unmasked pairs).
 Printed on stdout as ONE JSON line, with:
   roofline      the dominant kernel's useful TFLOP/s against bf16 dense MFMA
                 peak (events on the launch stream, averaged over the timed
-                steps);
+                steps); traffic = its HBM bytes per launch from the committed
+                rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+                (profiles/hbm_traffic_pmc.md);
   cpu_baseline  the fp32 eager oracle's fwd+bwd on the host cores over a
                 bounded sample of (b, h) slices of the same workload;
   decode        configs[3]: split-KV decode KV-read GB/s at splits
@@ -49,6 +51,21 @@ def log(msg: str) -> None:
 
 def useful_fwd_flops(B, H, n, bs):
     return 4 * D * B * H * (n * n + n * bs)
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (profiles/hbm_traffic_pmc.md, calibrated
+    against a copy of known size), or None if it is not there."""
+    path = REPO / "profiles" / "hbm_traffic_pmc.md"
+    try:
+        for line in path.read_text().splitlines():
+            parts = line.split()
+            if len(parts) == 3 and parts[0] == "traffic" and parts[1] == kernel:
+                return int(parts[2])
+    except OSError:
+        pass
+    return None
 
 
 def seeded_bf16(shape, seed, count, device):
@@ -220,7 +237,7 @@ def decode_bench(device, reps: int):
         "kv_bytes": kv_bytes,
         "rows": rows,
         "roofline": {"bound": "hbm", "achieved": best["GB_s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": best["GB_s"] / PEAK_HBM_GBS, "traffic": None,
+                     "frac": best["GB_s"] / PEAK_HBM_GBS, "traffic": measured_traffic("decode16_partial"),
                      "kernel": f"bd3_decode_splitkv n_splits={best['n_splits']} ({best['rule']})"},
     }
 
@@ -279,9 +296,9 @@ def main(argv=None) -> int:
     # S, dP, dV, dK).
     fwd_flops = useful_fwd_flops(B, H, n, bs)
     kernels = {
-        "attn_fwd_kernel (bd3_attn_fwd)": (fwd_flops, per["fwd"]),
-        "attn_bwd_dq_kernel (bd3_attn_bwd_dq)": (1.5 * fwd_flops, per["bwd_dq"]),
-        "attn_bwd_dkdv_kernel (bd3_attn_bwd_dkdv)": (2.0 * fwd_flops, per["bwd_dkdv"]),
+        "attn_fwd_kernel": (fwd_flops, per["fwd"]),
+        "attn_bwd_dq_kernel": (1.5 * fwd_flops, per["bwd_dq"]),
+        "attn_bwd_dkdv_kernel": (2.0 * fwd_flops, per["bwd_dkdv"]),
     }
     dom_name, (dom_flops, dom_ms) = max(kernels.items(), key=lambda kv: kv[1][1])
     achieved = dom_flops / (dom_ms * 1e-3) / 1e12
@@ -307,8 +324,8 @@ def main(argv=None) -> int:
         "kernel_tflops": {k: f / (t * 1e-3) / 1e12 for k, (f, t) in kernels.items()},
         "useful_fraction_of_executed": census[0] / census[1],
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None, "kernel": dom_name,
-                     "algorithmic_flops_per_launch": dom_flops},
+                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": measured_traffic(dom_name),
+                     "kernel": dom_name, "algorithmic_flops_per_launch": dom_flops},
     }
     del step
     torch.cuda.empty_cache()

@@ -10,6 +10,9 @@
 //   in turn; each wave runs an online softmax over its chunks, then the four
 //   states are merged through LDS. With one split the workgroup writes O
 //   directly; otherwise it writes a normalised fp32 partial and its log2-LSE.
+//   K and V are read once per call, with non-temporal loads (ld16_stream) so
+//   the stream does not evict other data from L2 / MALL; measured 7% faster
+//   than cached loads at the configs[3] shape.
 //   S^T (32 keys x 32 rows) = K Q^T on v_mfma_f32_32x32x16_bf16 with K read
 //   from HBM straight into A-operand registers (one 16-byte load per lane and
 //   operand: a 128-byte key row is covered by 8 consecutive lanes' loads);
@@ -93,7 +96,7 @@ __global__ __launch_bounds__(kThreads) void decode_partial(DecodeArgs a) {
       const int key = imin(c0 + 32 * sb + l32, a.kv_len - 1);
 #pragma unroll
       for (int c = 0; c < 4; ++c)
-        kop[sb][c] = __builtin_bit_cast(bf16x8, ld16(kp + (int64_t)key * a.sk.s + 16 * c + 8 * g));
+        kop[sb][c] = __builtin_bit_cast(bf16x8, ld16_stream(kp + (int64_t)key * a.sk.s + 16 * c + 8 * g));
     }
     // V chunk -> wave-private LDS (row-major), 8 lanes per 128-byte row.
     u32x4 vbuf[8];
@@ -101,7 +104,7 @@ __global__ __launch_bounds__(kThreads) void decode_partial(DecodeArgs a) {
     for (int j = 0; j < 8; ++j) {
       const int e = lane + 64 * j;
       const int key = imin(c0 + (e >> 3), a.kv_len - 1);
-      vbuf[j] = ld16(vp + (int64_t)key * a.sv.s + (e & 7) * 8);
+      vbuf[j] = ld16_stream(vp + (int64_t)key * a.sv.s + (e & 7) * 8);
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -292,12 +295,12 @@ __global__ __launch_bounds__(kThreads, BD3_DEC16_OCC) void decode16_partial(Deco
     for (int kb = 0; kb < 4; ++kb) {
       const int key = imin(c0 + 16 * kb + l16, a.kv_len - 1);
 #pragma unroll
-      for (int c = 0; c < 2; ++c) cb.k[kb][c] = ld16(kp + (int64_t)key * a.sk.s + 32 * c + 8 * hq);
+      for (int c = 0; c < 2; ++c) cb.k[kb][c] = ld16_stream(kp + (int64_t)key * a.sk.s + 32 * c + 8 * hq);
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int key = imin(c0 + (lane >> 3) + 8 * j, a.kv_len - 1);
-      cb.v[j] = ld16(vp + (int64_t)key * a.sv.s + 8 * (lane & 7));
+      cb.v[j] = ld16_stream(vp + (int64_t)key * a.sv.s + 8 * (lane & 7));
     }
   };
 

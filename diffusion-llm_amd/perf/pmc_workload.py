@@ -1,0 +1,80 @@
+"""Short, fixed workload for rocprofv3 counter runs (--pmc).
+
+    rocprofv3 --pmc FETCH_SIZE -- python3 diffusion-llm_amd/perf/pmc_workload.py
+
+Dispatches, in order and each `--reps` times:
+  1. a plain device copy of --copy-mib MiB (torch copy_) - the calibration
+     kernel: its FETCH_SIZE / WRITE_SIZE per dispatch against its known
+     byte count gives the factor that turns the counters into bytes;
+  2. the training forward, dQ and dK/dV kernels, by default at BASELINE
+     configs[1] (B=8, L=1024, H=12, d=64, block 16, bf16; --batch, --heads,
+     --seq-len and --block-size change the shape);
+  3. the split-KV decode at configs[3] (32 x 12 heads, q_len 16,
+     kv_len 4112) with the library's automatic split count.
+No timing is done here; the profiler records per-dispatch counters.
+"""
+from __future__ import annotations
+
+import argparse
+import sys
+from pathlib import Path
+
+_HERE = Path(__file__).resolve()
+for _p in (str(_HERE.parents[2]), str(_HERE.parents[1])):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--reps", type=int, default=3)
+    ap.add_argument("--copy-mib", type=int, default=256)
+    ap.add_argument("--batch", type=int, default=8)
+    ap.add_argument("--heads", type=int, default=12)
+    ap.add_argument("--seq-len", type=int, default=1024)
+    ap.add_argument("--block-size", type=int, default=16)
+    ap.add_argument("--no-decode", action="store_true")
+    args = ap.parse_args(argv)
+
+    import torch
+    from bench import TrainStep, seeded_bf16
+    from kernels._native import check, lib, ptr, stream_of, strides
+
+    dev = torch.device("cuda:0")
+    n_el = args.copy_mib * (1 << 20) // 4
+    src = torch.ones(n_el, device=dev, dtype=torch.float32)
+    dst = torch.empty_like(src)
+    for _ in range(args.reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"copy calibration: {args.copy_mib} MiB read + {args.copy_mib} MiB written per dispatch", flush=True)
+
+    step = TrainStep(args.batch, args.heads, args.seq_len, args.block_size, dev)
+    for _ in range(args.reps):
+        step.fwd()
+        step.bwd_dq()
+        step.bwd_dkdv()
+    torch.cuda.synchronize()
+    print("training kernels done", flush=True)
+    del step
+
+    if args.no_decode:
+        return 0
+    B, H, q_len, kv_len, bs, D = 32, 12, 16, 4112, 16, 64
+    q = seeded_bf16((B, H, q_len, D), 0, 1, dev)[0]
+    k, v = seeded_bf16((B, H, kv_len, D), 1, 2, dev)
+    o = torch.empty_like(q)
+    L = lib()
+    nbytes = L.bd3_decode_workspace_bytes(B, H, q_len, kv_len, D, 0)
+    ws = torch.empty(max(nbytes, 1), device=dev, dtype=torch.uint8)
+    st = strides(q, k, v, o)
+    for _ in range(args.reps):
+        check(L.bd3_decode(ptr(q), ptr(k), ptr(v), ptr(o), B, H, q_len, kv_len, D, bs, st, 1.0 / 8,
+                           ptr(ws), nbytes, stream_of(q)))
+    torch.cuda.synchronize()
+    print(f"decode done (K+V bytes per dispatch {2 * B * H * kv_len * D * 2})", flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
