@@ -296,9 +296,9 @@ def main(argv=None) -> int:
     # S, dP, dV, dK).
     fwd_flops = useful_fwd_flops(B, H, n, bs)
     kernels = {
-        "attn_fwd_kernel": (fwd_flops, per["fwd"]),
-        "attn_bwd_dq_kernel": (1.5 * fwd_flops, per["bwd_dq"]),
-        "attn_bwd_dkdv_kernel": (2.0 * fwd_flops, per["bwd_dkdv"]),
+        "attn_fwd_dma_kernel": (fwd_flops, per["fwd"]),
+        "attn_bwd_dq_dma_kernel": (1.5 * fwd_flops, per["bwd_dq"]),
+        "attn_bwd_dkdv_dma_kernel": (2.0 * fwd_flops, per["bwd_dkdv"]),
     }
     dom_name, (dom_flops, dom_ms) = max(kernels.items(), key=lambda kv: kv[1][1])
     achieved = dom_flops / (dom_ms * 1e-3) / 1e12

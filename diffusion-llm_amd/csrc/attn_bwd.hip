@@ -26,6 +26,7 @@
 #include "bd3_device.h"
 #include "bd3_launch.h"
 #include "bd3_mask.h"
+#include "bd3_swz.h"
 #include "bd3_tile.h"
 
 namespace bd3 {
@@ -399,6 +400,404 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_bwd_dkdv_kernel(BwdArgs a) 
   }
 }
 
+// ---------------------------------------------------------------------------
+// Key-stationary dK/dV with direct loads: same products and numerics as
+// attn_bwd_dkdv_kernel<4, 1, OCC>, but the query tiles (Q, dO and the rows'
+// L and Delta) go global -> LDS with global_load_lds into a three-stage ring
+// of swizzled tiles, two tiles ahead, with one counted vmcnt wait and barrier
+// per tile. Every live tile runs one code path over both of its 32-row
+// blocks; a block that is not fully visible to the wave's keys is masked in
+// place (MASK16: block size a multiple of 16, two tests per lane).
+template <int OCC, bool MASK16>
+__global__ __launch_bounds__(256, OCC) void attn_bwd_dkdv_dma_kernel(BwdArgs a) {
+  constexpr int kBK = 128;  // keys per workgroup: 4 waves x 32
+  constexpr int kStages = 3;
+  // Stage layout (bytes): Q tile [0, 8K), dO tile [8K, 16K), row scalars
+  // [16K, 17K): L of the 64 rows, then Delta, then both again (the load that
+  // fetches them writes 1 KB).
+  constexpr int kStageBytes = 4 * kSwTile + 1024;
+  __shared__ __attribute__((aligned(1024))) __bf16 smem[kStages * kStageBytes / 2];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = wave_uniform(tid >> 6);
+  const int l32 = lane & 31;
+  const int g = lane >> 5;
+
+  // Heaviest key tiles first: clean tiles are seen by the most rows.
+  const BlockOrder bo(a.bh, a.heads);
+  const int tiles_half = a.n / kBK;
+  const int k0 = bo.rank < tiles_half ? a.n + bo.rank * kBK : (bo.rank - tiles_half) * kBK;
+
+  const uint16_t* qp = uniform_ptr(a.q + bo.b * a.sq.b + bo.h * a.sq.h);
+  const uint16_t* dop = uniform_ptr(a.dout + bo.b * a.sdo.b + bo.h * a.sdo.h);
+  const uint16_t* kp = a.k + bo.b * a.sk.b + bo.h * a.sk.h;
+  const uint16_t* vp = a.v + bo.b * a.sv.b + bo.h * a.sv.h;
+  const int64_t rowbase = (int64_t)bo.bh * 2 * a.n;
+
+  const int kw = k0 + 32 * wave;
+  const int key = kw + l32;
+  bf16x8 kreg[4], vreg[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    kreg[c] = __builtin_bit_cast(bf16x8, ld16(kp + (int64_t)key * a.sk.s + 16 * c + 8 * g));
+    vreg[c] = __builtin_bit_cast(bf16x8, ld16(vp + (int64_t)key * a.sv.s + 16 * c + 8 * g));
+  }
+
+  const KeyRanges qr = train_query_ranges(k0, kBK, a.n, a.bs, kSwRows);
+  const int t0 = wave_uniform(qr.t0), t2 = wave_uniform(qr.t2);
+  const int n_first = wave_uniform(qr.t1 - qr.t0);
+  const int n_tiles = n_first + wave_uniform(qr.t3 - qr.t2);
+  auto tile_of = [&](int i) { return i < n_first ? t0 + i : t2 + (i - n_first); };
+
+  // Wave w fills 1 KB blocks 2w, 2w+1 (rows 16w .. 16w+15) of the Q and dO
+  // tiles; wave 0 also fetches the row scalars: lane L reads 16 bytes of L
+  // (L % 32 < 16) or Delta, rows 4 (L % 16) .. +3.
+  uint32_t qoff[2], dooff[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int r = 16 * wave + 8 * j + (lane >> 3);
+    const int ch = 8 * ((lane & 7) ^ swz(r));
+    qoff[j] = (uint32_t)(2 * (r * (int)a.sq.s + ch));
+    dooff[j] = (uint32_t)(2 * (r * (int)a.sdo.s + ch));
+  }
+  const float* scal_src = ((lane & 16) ? a.delta : a.lse) + rowbase + 4 * (lane & 15);
+  const int64_t qstep = (int64_t)kSwRows * a.sq.s, dostep = (int64_t)kSwRows * a.sdo.s;
+  const uint32_t lds0 = lds_addr(&smem[0]);
+  auto issue = [&](int i, int stage) {
+    const int64_t tl = wave_uniform(tile_of(i));
+    const uint32_t st = lds0 + (uint32_t)(stage * kStageBytes) + (uint32_t)wave * 2048u;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) dma16(qp + tl * qstep, qoff[j], st + 1024u * j);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) dma16(dop + tl * dostep, dooff[j], st + 8192u + 1024u * j);
+    if (wave == 0) dma16_va(scal_src + tl * kSwRows, lds0 + (uint32_t)(stage * kStageBytes) + 16384u);
+  };
+  // Wave 0 has one more load per tile in flight than the others.
+  auto wait_barrier = [&](bool in_flight) {
+    if (!in_flight)
+      vm_wait_barrier<0>();
+    else if (wave == 0)
+      vm_wait_barrier<5>();
+    else
+      vm_wait_barrier<4>();
+  };
+
+  // Tiles 0 and 1 are requested before the K / V rows are waited for.
+  issue(0, 0);
+  if (n_tiles > 1) issue(1, 1);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) asm volatile("" ::"v"(kreg[c]), "v"(vreg[c]));
+  const RowIntervals civ = train_col_intervals(key, a.n, a.bs);
+  const ClassBounds cb = uniform_bounds(key_group_bounds(train_key_group(kw, 32, a.n, a.bs), a.n));
+
+  f32x16 dk[2] = {}, dv[2] = {};  // [d block]: lane = d column, registers = keys
+
+  // P^T and dS^T operands of one 32-row block qb of the current query tile:
+  // S, dP (rows x keys, lane = key column, register r <-> row
+  // 32qb + 8(r/4) + 4g + r%4), P, dS. A block that is not fully visible gets
+  // P = 0 on its invisible pairs: with MASK16 (block size a multiple of 16)
+  // the mask is constant on 16-row x 1-key strips, so one test per lane for
+  // rows 0-15 of the block (registers 0-7) and one for rows 16-31 decide it;
+  // otherwise every pair is tested. A dead block is computed and fully masked.
+  auto block_ops = [&](const __bf16* qs, const __bf16* dos, const float* scal, int q0, int qb, bool masked,
+                       bf16x8 (&pop)[2], bf16x8 (&dsop)[2]) {
+    bf16x8 qa[4], da[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      qa[c] = sw_row_op(qs, 32 * qb, c, lane);
+      da[c] = sw_row_op(dos, 32 * qb, c, lane);
+    }
+    f32x16 s = {}, dp = {};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      s = mfma32(qa[c], kreg[c], s);
+      dp = mfma32(da[c], vreg[c], dp);
+    }
+    float p[16];
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) {
+      const f32x4 lr = *reinterpret_cast<const f32x4*>(&scal[32 * qb + 8 * rg + 4 * g]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) p[4 * rg + j] = fast_exp2(fmaf(s[4 * rg + j], a.scale_log2, -lr[j] * kLog2e));
+    }
+    if (masked) {
+      if (MASK16) {
+        const bool lo = iv_has(civ, q0 + 32 * qb), hi = iv_has(civ, q0 + 32 * qb + 16);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) p[r] = (r < 8 ? lo : hi) ? p[r] : 0.f;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          p[r] = iv_has(civ, q0 + 32 * qb + 8 * (r >> 2) + 4 * g + (r & 3)) ? p[r] : 0.f;
+      }
+    }
+    float ds[16];
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) {
+      const f32x4 dr = *reinterpret_cast<const f32x4*>(&scal[64 + 32 * qb + 8 * rg + 4 * g]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) ds[4 * rg + j] = p[4 * rg + j] * (dp[4 * rg + j] - dr[j]);
+    }
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc) {
+      pop[kc] = to_bf16x8(p[8 * kc], p[8 * kc + 1], p[8 * kc + 2], p[8 * kc + 3], p[8 * kc + 4], p[8 * kc + 5],
+                          p[8 * kc + 6], p[8 * kc + 7]);
+      dsop[kc] = to_bf16x8(ds[8 * kc], ds[8 * kc + 1], ds[8 * kc + 2], ds[8 * kc + 3], ds[8 * kc + 4],
+                           ds[8 * kc + 5], ds[8 * kc + 6], ds[8 * kc + 7]);
+    }
+  };
+
+  // Every key group is seen by its own block, so n_tiles >= 1.
+  vm_wait_barrier<0>();
+  int cur = 0;
+  for (int it = 0; it < n_tiles; ++it) {
+    const bool pf = it + 2 < n_tiles;
+    if (pf) issue(it + 2, cur == 0 ? 2 : cur - 1);
+    const int q0 = wave_uniform(tile_of(it) * kSwRows);
+    const int c0 = bounds_class(cb, q0, 32, a.n);
+    const int c1 = bounds_class(cb, q0 + 32, 32, a.n);
+    // One code path for every live tile (the accumulators are updated by one
+    // set of instructions, so they keep their registers).
+    if ((c0 | c1) != kNone) {
+      const __bf16* qs = &smem[cur * (kStageBytes / 2)];
+      const __bf16* dos = qs + kSwTile;
+      const float* scal = reinterpret_cast<const float*>(qs + 2 * kSwTile);
+      bf16x8 pop[2][2], dsop[2][2];  // [row block][16-row step]
+      block_ops(qs, dos, scal, q0, 0, c0 != kFull, pop[0], dsop[0]);
+      block_ops(qs, dos, scal, q0, 1, c1 != kFull, pop[1], dsop[1]);
+      // dV += P^T dO, dK += dS^T Q with dO / Q read transposed.
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+          for (int db = 0; db < 2; ++db) {
+            const bf16x8 dot = sw_tr_op(dos, 32 * qb + 16 * kc, 32 * db, lane);
+            const bf16x8 qt = sw_tr_op(qs, 32 * qb + 16 * kc, 32 * db, lane);
+            dv[db] = mfma32(pop[qb][kc], dot, dv[db]);
+            dk[db] = mfma32(dsop[qb][kc], qt, dk[db]);
+          }
+    }
+    wait_barrier(pf);
+    cur = cur == 2 ? 0 : cur + 1;
+  }
+
+  // Epilogue (every wave is past the last barrier, no load in flight): each
+  // wave transposes its 32 keys x 64 d of dK, then dV, through its own padded
+  // LDS slice into row-major bf16, then writes 16-byte row chunks.
+  __bf16* tile = &smem[0] + wave * kTileElems;
+  uint16_t* outs[2] = {a.dk + bo.b * a.sdk.b + bo.h * a.sdk.h, a.dv + bo.b * a.sdv.b + bo.h * a.sdv.h};
+  const int64_t ostr[2] = {a.sdk.s, a.sdv.s};
+#pragma unroll
+  for (int which = 0; which < 2; ++which) {
+    const float mul = which == 0 ? a.scale : 1.f;
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int krow = 8 * (r >> 2) + 4 * g + (r & 3);
+        const float x = (which == 0 ? dk[db][r] : dv[db][r]) * mul;
+        tile[krow * kLdsStride + 32 * db + l32] = (__bf16)x;
+      }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = (lane >> 3) + 8 * j;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(&tile[row * kLdsStride + 8 * (lane & 7)]);
+      st16(outs[which] + (int64_t)(kw + row) * ostr[which] + 8 * (lane & 7), v);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Query-stationary dQ (and Delta) with direct loads: same products and
+// numerics as attn_bwd_dq_kernel<4, 1, OCC>. K / V key tiles go global -> LDS
+// with global_load_lds into a three-stage ring of swizzled tiles, two tiles
+// ahead. Every live tile runs one code path over both of its 32-key blocks;
+// a block that is not fully visible to the wave's rows is masked in place
+// (MASK16: block size a multiple of 16, two tests per lane).
+template <int OCC, bool MASK16>
+__global__ __launch_bounds__(256, OCC) void attn_bwd_dq_dma_kernel(BwdArgs a) {
+  constexpr int kBM = 128;  // query rows per workgroup: 4 waves x 32
+  constexpr int kStages = 3;
+  __shared__ __attribute__((aligned(1024))) __bf16 smem[kStages][2][kSwTile];  // [stage][K|V]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = wave_uniform(tid >> 6);
+  const int l32 = lane & 31;
+  const int g = lane >> 5;
+
+  const BlockOrder bo(a.bh, a.heads);
+  const int tiles_half = a.n / kBM;
+  const int t = tiles_half - 1 - (bo.rank >> 1);
+  const int q0 = ((bo.rank & 1) ? 0 : a.n) + t * kBM;
+
+  const uint16_t* qp = a.q + bo.b * a.sq.b + bo.h * a.sq.h;
+  const uint16_t* kp = uniform_ptr(a.k + bo.b * a.sk.b + bo.h * a.sk.h);
+  const uint16_t* vp = uniform_ptr(a.v + bo.b * a.sv.b + bo.h * a.sv.h);
+  const uint16_t* opp = a.o + bo.b * a.so.b + bo.h * a.so.h;
+  const uint16_t* dop = a.dout + bo.b * a.sdo.b + bo.h * a.sdo.h;
+  const int64_t rowbase = (int64_t)bo.bh * 2 * a.n;
+
+  const int qrow0 = q0 + 32 * wave;
+  const int myq = qrow0 + l32;
+  bf16x8 qreg[4], doreg[4], oreg[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int col = 16 * c + 8 * g;
+    qreg[c] = __builtin_bit_cast(bf16x8, ld16(qp + (int64_t)myq * a.sq.s + col));
+    doreg[c] = __builtin_bit_cast(bf16x8, ld16(dop + (int64_t)myq * a.sdo.s + col));
+    oreg[c] = __builtin_bit_cast(bf16x8, ld16(opp + (int64_t)myq * a.so.s + col));
+  }
+  const float lse_row = a.lse[rowbase + myq];
+
+  const KeyRanges kr = train_key_ranges(q0, kBM, a.n, a.bs, kSwRows);
+  const int t0 = wave_uniform(kr.t0), t2 = wave_uniform(kr.t2);
+  const int n_first = wave_uniform(kr.t1 - kr.t0);
+  const int n_tiles = n_first + wave_uniform(kr.t3 - kr.t2);
+  auto tile_of = [&](int i) { return i < n_first ? t0 + i : t2 + (i - n_first); };
+
+  // Wave w fills 1 KB blocks 2w, 2w+1 (rows 16w .. 16w+15) of the K and V tiles.
+  uint32_t koff[2], voff[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int r = 16 * wave + 8 * j + (lane >> 3);
+    const int ch = 8 * ((lane & 7) ^ swz(r));
+    koff[j] = (uint32_t)(2 * (r * (int)a.sk.s + ch));
+    voff[j] = (uint32_t)(2 * (r * (int)a.sv.s + ch));
+  }
+  const int64_t kstep = (int64_t)kSwRows * a.sk.s, vstep = (int64_t)kSwRows * a.sv.s;
+  const uint32_t lds_w = lds_addr(&smem[0][0][0]) + (uint32_t)wave * 2048u;
+  auto issue = [&](int i, int stage) {
+    const int64_t tl = wave_uniform(tile_of(i));
+    const uint32_t dst = lds_w + (uint32_t)stage * 16384u;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) dma16(kp + tl * kstep, koff[j], dst + 1024u * j);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) dma16(vp + tl * vstep, voff[j], dst + 8192u + 1024u * j);
+  };
+
+  // Tiles 0 and 1 are requested before the row loads are waited for.
+  issue(0, 0);
+  if (n_tiles > 1) issue(1, 1);
+  // Delta = rowsum(dO o O) (the reference's separate op), stored for dK/dV.
+  float dsum = 0.f;
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dsum = fmaf((float)doreg[c][j], (float)oreg[c][j], dsum);
+  const float drow = sum_xor32(dsum);
+  const float lrow = lse_row * kLog2e;
+  if (g == 0) a.delta[rowbase + myq] = drow;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) asm volatile("" ::"v"(qreg[c]), "v"(doreg[c]));
+  const RowIntervals riv = train_row_intervals(myq, a.n, a.bs);
+  const ClassBounds cb = uniform_bounds(row_group_bounds(train_row_group(qrow0, 32, a.n, a.bs), a.n));
+
+  f32x16 dq[2] = {};  // dQ^T [d block]
+
+  // dS^T operands of one 32-key block sb of the current tile: S^T, dP^T
+  // (keys x rows, lane = row, register r <-> key k0 + 32sb + 8(r/4) + 4g +
+  // r%4), P, dS. A block that is not fully visible gets P = 0 on its
+  // invisible pairs: with MASK16 (block size a multiple of 16) the mask is
+  // constant on 1-row x 16-key strips, so one test per lane for keys 0-15 of
+  // the block (registers 0-7) and one for keys 16-31 decide it; otherwise
+  // every pair is tested. A dead block is computed and fully masked.
+  auto block_ops = [&](const __bf16* ks, const __bf16* vs, int k0, int sb, bool masked, bf16x8 (&dsop)[2]) {
+    bf16x8 kop[4], vop[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      kop[c] = sw_row_op(ks, 32 * sb, c, lane);
+      vop[c] = sw_row_op(vs, 32 * sb, c, lane);
+    }
+    f32x16 s = {}, dp = {};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      s = mfma32(kop[c], qreg[c], s);
+      dp = mfma32(vop[c], doreg[c], dp);
+    }
+    float p[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) p[r] = fast_exp2(fmaf(s[r], a.scale_log2, -lrow));
+    if (masked) {
+      if (MASK16) {
+        const bool lo = iv_has(riv, k0 + 32 * sb), hi = iv_has(riv, k0 + 32 * sb + 16);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) p[r] = (r < 8 ? lo : hi) ? p[r] : 0.f;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          p[r] = iv_has(riv, k0 + 32 * sb + 8 * (r >> 2) + 4 * g + (r & 3)) ? p[r] : 0.f;
+      }
+    }
+    float ds[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) ds[r] = p[r] * (dp[r] - drow);
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc)
+      dsop[kc] = to_bf16x8(ds[8 * kc], ds[8 * kc + 1], ds[8 * kc + 2], ds[8 * kc + 3], ds[8 * kc + 4],
+                           ds[8 * kc + 5], ds[8 * kc + 6], ds[8 * kc + 7]);
+  };
+
+  // Every row group sees at least its own block, so n_tiles >= 1.
+  vm_wait_barrier<0>();
+  int cur = 0;
+  for (int it = 0; it < n_tiles; ++it) {
+    const bool pf = it + 2 < n_tiles;
+    if (pf) issue(it + 2, cur == 0 ? 2 : cur - 1);
+    const int k0 = wave_uniform(tile_of(it) * kSwRows);
+    const int c0 = bounds_class(cb, k0, 32, a.n);
+    const int c1 = bounds_class(cb, k0 + 32, 32, a.n);
+    // One code path for every live tile (the accumulators keep their registers).
+    if ((c0 | c1) != kNone) {
+      const __bf16* ks = smem[cur][0];
+      const __bf16* vs = smem[cur][1];
+      bf16x8 dsop[2][2];  // [key block][16-key step]
+      block_ops(ks, vs, k0, 0, c0 != kFull, dsop[0]);
+      block_ops(ks, vs, k0, 1, c1 != kFull, dsop[1]);
+      // dQ^T += K^T dS^T with K^T read transposed.
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+          for (int db = 0; db < 2; ++db)
+            dq[db] = mfma32(sw_tr_op(ks, 32 * sb + 16 * kc, 32 * db, lane), dsop[sb][kc], dq[db]);
+    }
+    if (pf)
+      vm_wait_barrier<4>();
+    else
+      vm_wait_barrier<0>();
+    cur = cur == 2 ? 0 : cur + 1;
+  }
+
+  uint16_t* dqp = a.dq + bo.b * a.sdq.b + bo.h * a.sdq.h + (int64_t)myq * a.sdq.s;
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg)
+      *reinterpret_cast<bf16x4*>(dqp + 32 * db + 8 * rg + 4 * g) =
+          to_bf16x4(dq[db][4 * rg] * a.scale, dq[db][4 * rg + 1] * a.scale, dq[db][4 * rg + 2] * a.scale,
+                    dq[db][4 * rg + 3] * a.scale);
+}
+
+#ifndef BD3_DQ_DMA
+#define BD3_DQ_DMA 1
+#endif
+#ifndef BD3_DQ_DMA_OCC
+#define BD3_DQ_DMA_OCC 3
+#endif
+#ifndef BD3_KV_DMA
+#define BD3_KV_DMA 1
+#endif
+#ifndef BD3_KV_DMA_OCC
+#define BD3_KV_DMA_OCC 2
+#endif
 #ifndef BD3_DQ_NW
 #define BD3_DQ_NW 4
 #endif
@@ -422,7 +821,14 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_bwd_dkdv_kernel(BwdArgs a) 
 
 hipError_t launch_attn_bwd_dq(const BwdArgs& a, hipStream_t stream) {
   constexpr int kNW = BD3_DQ_NW, kRB = BD3_DQ_RB, kOcc = BD3_DQ_OCC, kBM = 32 * kNW * kRB;
-  if (a.n % kBM == 0)
+  if (BD3_DQ_DMA)  // n % 128 == 0 always holds (validated)
+    if (a.bs % 16 == 0)
+      hipLaunchKernelGGL((attn_bwd_dq_dma_kernel<BD3_DQ_DMA_OCC, true>), dim3(a.bh * (2 * a.n / 128)), dim3(256),
+                         0, stream, a);
+    else
+      hipLaunchKernelGGL((attn_bwd_dq_dma_kernel<BD3_DQ_DMA_OCC, false>), dim3(a.bh * (2 * a.n / 128)), dim3(256),
+                         0, stream, a);
+  else if (a.n % kBM == 0)
     hipLaunchKernelGGL((attn_bwd_dq_kernel<kNW, kRB, kOcc>), dim3(a.bh * (2 * a.n / kBM)), dim3(kNW * 64), 0,
                        stream, a);
   else  // n % 128 == 0 always holds (validated)
@@ -432,7 +838,14 @@ hipError_t launch_attn_bwd_dq(const BwdArgs& a, hipStream_t stream) {
 
 hipError_t launch_attn_bwd_dkdv(const BwdArgs& a, hipStream_t stream) {
   constexpr int kNW = BD3_KV_NW, kKB = BD3_KV_KB, kOcc = BD3_KV_OCC, kBK = 32 * kNW * kKB;
-  if (a.n % kBK == 0)
+  if (BD3_KV_DMA)  // n % 128 == 0 always holds (validated)
+    if (a.bs % 16 == 0)
+      hipLaunchKernelGGL((attn_bwd_dkdv_dma_kernel<BD3_KV_DMA_OCC, true>), dim3(a.bh * (2 * a.n / 128)), dim3(256),
+                         0, stream, a);
+    else
+      hipLaunchKernelGGL((attn_bwd_dkdv_dma_kernel<BD3_KV_DMA_OCC, false>), dim3(a.bh * (2 * a.n / 128)), dim3(256),
+                         0, stream, a);
+  else if (a.n % kBK == 0)
     hipLaunchKernelGGL((attn_bwd_dkdv_kernel<kNW, kKB, kOcc>), dim3(a.bh * (2 * a.n / kBK)), dim3(kNW * 64), 0,
                        stream, a);
   else

@@ -28,6 +28,7 @@
 #include "bd3_device.h"
 #include "bd3_launch.h"
 #include "bd3_mask.h"
+#include "bd3_swz.h"
 #include "bd3_tile.h"
 
 namespace bd3 {
@@ -232,21 +233,25 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_kernel(FwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Software-pipelined forward, one 32-row block per wave. Iteration i issues
-// the S^T MFMAs of key tile i+1 before the softmax and PV of tile i, so the
-// matrix cores work while the VALU runs the softmax; tile i+2 is meanwhile
-// loaded into registers. LDS holds two tiles: K of a stage is consumed one
-// iteration before its V, so a stage is refilled (between two barriers) right
-// after the PV that reads its V. Each tile is classified for the wave as dead
-// (skipped), full (no mask) or masked (interval mask, which also zeroes a dead
-// 32-key half), so each path is straight-line code.
-enum WaveTile { kTileDead = 0, kTileFull = 1, kTileMasked = 2 };
-
-template <int NW, int OCC>
-__global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_pipe_kernel(FwdArgs a) {
-  constexpr int kThreads = NW * 64;
-  constexpr int kBM = 32 * NW;
-  __shared__ __attribute__((aligned(16))) __bf16 smem[2][2][kTileElems];  // [stage][K|V]
+// Direct-load forward. The per-wave critical path of the staged kernel above
+// is mostly exposed latency (a single wave per SIMD takes as long per key
+// tile as three), so this variant shortens it:
+//   * K/V tiles go global -> LDS with global_load_lds_dwordx4 into a
+//     three-stage ring of swizzled tiles (bd3_swz.h), two tiles ahead; no
+//     VGPR staging, no LDS store pass, one counted vmcnt wait + barrier per
+//     tile (the barrier is plain s_barrier: the loads of the tile after next
+//     stay in flight across it);
+//   * all K operands of a tile are read from LDS in one batch, and the V^T
+//     operands are requested right after the S^T products are issued, so
+//     their latency hides behind the softmax;
+//   * one wave-uniform class per 64-key tile (dead / full / partial): a full
+//     tile runs straight-line code with no mask arithmetic.
+// Numerics are those of attn_fwd_kernel (same products, same lazy rescale).
+template <int OCC>
+__global__ __launch_bounds__(256, OCC) void attn_fwd_dma_kernel(FwdArgs a) {
+  constexpr int kBM = 128;  // query rows per workgroup: 4 waves x 32
+  constexpr int kStages = 3;
+  __shared__ __attribute__((aligned(1024))) __bf16 smem[kStages][2][kSwTile];  // [stage][K|V]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -260,142 +265,141 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_pipe_kernel(FwdArgs a) 
   const int q0 = ((bo.rank & 1) ? 0 : a.n) + t * kBM;
 
   const uint16_t* qp = a.q + bo.b * a.sq.b + bo.h * a.sq.h;
-  const uint16_t* kp = a.k + bo.b * a.sk.b + bo.h * a.sk.h;
-  const uint16_t* vp = a.v + bo.b * a.sv.b + bo.h * a.sv.h;
+  const uint16_t* kp = uniform_ptr(a.k + bo.b * a.sk.b + bo.h * a.sk.h);
+  const uint16_t* vp = uniform_ptr(a.v + bo.b * a.sv.b + bo.h * a.sv.h);
 
   const int qrow0 = q0 + 32 * wave;
   const int myq = qrow0 + l32;
-  const RowIntervals riv = train_row_intervals(myq, a.n, a.bs);
-  const RowGroup rg = uniform_row_group(qrow0, 32, a.n, a.bs);
   bf16x8 qreg[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c)
     qreg[c] = __builtin_bit_cast(bf16x8, ld16(qp + (int64_t)myq * a.sq.s + 16 * c + 8 * g));
 
-  const KeyRanges kr = train_key_ranges(q0, kBM, a.n, a.bs, kTileRows);
+  const KeyRanges kr = train_key_ranges(q0, kBM, a.n, a.bs, kSwRows);
   const int t0 = wave_uniform(kr.t0), t2 = wave_uniform(kr.t2);
   const int n_first = wave_uniform(kr.t1 - kr.t0);
   const int n_tiles = n_first + wave_uniform(kr.t3 - kr.t2);
   auto tile_of = [&](int i) { return i < n_first ? t0 + i : t2 + (i - n_first); };
 
-  TileStager<kThreads, 2> st;
-  {
-    const int64_t rs[2] = {a.sk.s, a.sv.s};
-    st.init(tid, rs);
-  }
-  auto stage_load = [&](int i) {
-    const int64_t k0 = (int64_t)tile_of(i) * kTileRows;
-    const uint16_t* base[2] = {kp + k0 * a.sk.s, vp + k0 * a.sv.s};
-    st.load(base);
-  };
-  auto stage_store = [&](int stage) {
-    __bf16* dst[2] = {smem[stage][0], smem[stage][1]};
-    st.store(dst);
-  };
-  auto tclass = [&](int i) {
-    const int k0 = wave_uniform(tile_of(i) * kTileRows);
-    const int c0 = row_group_class(rg, k0, 32, a.n);
-    const int c1 = row_group_class(rg, k0 + 32, 32, a.n);
-    const int r = (c0 | c1) == kNone ? kTileDead
-                                     : ((c0 == kFull && c1 == kFull) ? kTileFull : kTileMasked);
-    return wave_uniform(r);
-  };
-  auto mma_s = [&](const __bf16* ks, f32x16& s0, f32x16& s1) {
-    s0 = f32x16{};
-    s1 = f32x16{};
+  // Wave w fills the 1 KB blocks 2w and 2w+1 (rows 16w .. 16w+15) of each K
+  // and V tile: lane L fetches logical chunk (L%8) ^ swz(row) of row
+  // 16w + 8j + L/8 (byte offsets from the tile's row 0).
+  uint32_t koff[2], voff[2];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const bf16x8 k0op = lds_row_op(ks, 0, c, lane);
-      const bf16x8 k1op = lds_row_op(ks, 32, c, lane);
-      s0 = mfma32(k0op, qreg[c], s0);
-      s1 = mfma32(k1op, qreg[c], s1);
-    }
+  for (int j = 0; j < 2; ++j) {
+    const int r = 16 * wave + 8 * j + (lane >> 3);
+    const int ch = 8 * ((lane & 7) ^ swz(r));
+    koff[j] = (uint32_t)(2 * (r * (int)a.sk.s + ch));
+    voff[j] = (uint32_t)(2 * (r * (int)a.sv.s + ch));
+  }
+  const int64_t kstep = (int64_t)kSwRows * a.sk.s, vstep = (int64_t)kSwRows * a.sv.s;
+  // LDS byte address of this wave's first K block in stage 0; a stage is
+  // 2 * 8 KB (K then V).
+  const uint32_t lds_w = lds_addr(&smem[0][0][0]) + (uint32_t)wave * 2048u;
+  auto issue = [&](int i, int stage) {
+    const int64_t tl = wave_uniform(tile_of(i));
+    const uint16_t* kb = kp + tl * kstep;
+    const uint16_t* vb = vp + tl * vstep;
+    const uint32_t dst = lds_w + (uint32_t)stage * 16384u;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) dma16(kb, koff[j], dst + 1024u * j);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) dma16(vb, voff[j], dst + 8192u + 1024u * j);
   };
+
+  // The first two tiles are requested before waiting for Q, so the two
+  // latencies overlap. Consuming Q here (an empty asm reading it) makes the
+  // compiler place its own wait for the Q loads at this point; that wait
+  // also covers the direct loads issued after them, which is harmless.
+  issue(0, 0);
+  if (n_tiles > 1) issue(1, 1);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) asm volatile("" ::"v"(qreg[c]));
+  const RowIntervals riv = train_row_intervals(myq, a.n, a.bs);
+  const ClassBounds cb = uniform_bounds(row_group_bounds(train_row_group(qrow0, 32, a.n, a.bs), a.n));
 
   f32x16 o[2] = {};  // O^T [d block]
   float m = -INFINITY, lsum = 0.f;
 
-  auto soft_pv = [&](int i, int cls, f32x16& s0, f32x16& s1, const __bf16* vs) {
-    if (cls == kTileMasked) {
-      const int k0 = tile_of(i) * kTileRows;
+  // Every row group sees at least its own block, so n_tiles >= 1.
+  vm_wait_barrier<0>();
+
+  int cur = 0;
+  for (int it = 0; it < n_tiles; ++it) {
+    const bool pf = it + 2 < n_tiles;
+    if (pf) issue(it + 2, cur == 0 ? 2 : cur - 1);
+    const int k0 = wave_uniform(tile_of(it) * kSwRows);
+    const int cls = bounds_class(cb, k0, kSwRows, a.n);
+    if (cls != kNone) {
+      const __bf16* ks = smem[cur][0];
+      const __bf16* vs = smem[cur][1];
+      bf16x8 kop[2][4];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = k0 + 8 * (r >> 2) + 4 * g + (r & 3);
-        s0[r] = iv_has(riv, key) ? s0[r] : -INFINITY;
-        s1[r] = iv_has(riv, key + 32) ? s1[r] : -INFINITY;
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) kop[sb][c] = sw_row_op(ks, 32 * sb, c, lane);
+      f32x16 s[2] = {};
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) s[sb] = mfma32(kop[sb][c], qreg[c], s[sb]);
+      bf16x8 vop[2][2][2];  // [key block][16-key step][d block]
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+          for (int db = 0; db < 2; ++db) vop[sb][kc][db] = sw_tr_op(vs, 32 * sb + 16 * kc, 32 * db, lane);
+
+      if (cls == kPartial) {
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = k0 + 32 * sb + 8 * (r >> 2) + 4 * g + (r & 3);
+            s[sb][r] = iv_has(riv, key) ? s[sb][r] : -INFINITY;
+          }
       }
-    }
-    float mx = fmaxf(s0[0], s1[0]);
+      float mx = fmaxf(s[0][0], s[1][0]);
 #pragma unroll
-    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
-    const float mt = max_xor32(mx) * a.scale_log2;
-    if (__ballot(mt > m + kRescale) != 0) {
-      const float mn = fmaxf(m, mt);
-      const float alpha = (mn == -INFINITY) ? 1.f : fast_exp2(m - mn);
-      m = mn;
-      lsum *= alpha;
-      o[0] *= alpha;
-      o[1] *= alpha;
-    }
-    const float mu = (m == -INFINITY) ? 0.f : m;
-    float p0[16], p1[16];
+      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, fmaxf(s[0][r], s[1][r]));
+      const float mt = max_xor32(mx) * a.scale_log2;
+      if (__ballot(mt > m + kRescale) != 0) {
+        const float mn = fmaxf(m, mt);
+        const float alpha = (mn == -INFINITY) ? 1.f : fast_exp2(m - mn);
+        m = mn;
+        lsum *= alpha;
+        o[0] *= alpha;
+        o[1] *= alpha;
+      }
+      const float mu = (m == -INFINITY) ? 0.f : m;
+      bf16x8 pop[2][2];  // P^T operands [key block][16-key step]
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      p0[r] = fast_exp2(fmaf(s0[r], a.scale_log2, -mu));
-      p1[r] = fast_exp2(fmaf(s1[r], a.scale_log2, -mu));
-    }
-    bf16x8 pop[2][2];
+      for (int sb = 0; sb < 2; ++sb) {
+        float p[16];
 #pragma unroll
-    for (int kc = 0; kc < 2; ++kc) {
-      pop[0][kc] = to_bf16x8(p0[8 * kc], p0[8 * kc + 1], p0[8 * kc + 2], p0[8 * kc + 3],
-                             p0[8 * kc + 4], p0[8 * kc + 5], p0[8 * kc + 6], p0[8 * kc + 7]);
-      pop[1][kc] = to_bf16x8(p1[8 * kc], p1[8 * kc + 1], p1[8 * kc + 2], p1[8 * kc + 3],
-                             p1[8 * kc + 4], p1[8 * kc + 5], p1[8 * kc + 6], p1[8 * kc + 7]);
-      lsum = sum_bf16x8(pop[0][kc], lsum);
-      lsum = sum_bf16x8(pop[1][kc], lsum);
-    }
+        for (int r = 0; r < 16; ++r) p[r] = fast_exp2(fmaf(s[sb][r], a.scale_log2, -mu));
 #pragma unroll
-    for (int sb = 0; sb < 2; ++sb)
+        for (int kc = 0; kc < 2; ++kc) {
+          pop[sb][kc] = to_bf16x8(p[8 * kc], p[8 * kc + 1], p[8 * kc + 2], p[8 * kc + 3], p[8 * kc + 4],
+                                  p[8 * kc + 5], p[8 * kc + 6], p[8 * kc + 7]);
+          lsum = sum_bf16x8(pop[sb][kc], lsum);
+        }
+      }
 #pragma unroll
-      for (int kc = 0; kc < 2; ++kc)
+      for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
-        for (int db = 0; db < 2; ++db)
-          o[db] = mfma32(lds_tr_op(vs, 32 * sb + 16 * kc, 32 * db, lane), pop[sb][kc], o[db]);
-  };
-
-  // Prologue: tiles 0 and 1 into the two stages, S^T of tile 0.
-  stage_load(0);
-  stage_store(0);
-  if (n_tiles > 1) {
-    stage_load(1);
-    stage_store(1);
-  }
-  __syncthreads();
-  f32x16 sa0, sa1, sb0, sb1;
-  int ca = tclass(0), cb = kTileDead;
-  if (ca != kTileDead) mma_s(smem[0][0], sa0, sa1);
-
-  // One pipeline step: S^T of tile it+1, softmax + PV of tile it, refill.
-  auto step = [&](int it, int cur, f32x16& c0, f32x16& c1, int& nxt, f32x16& n0, f32x16& n1) {
-    const int stage = it & 1;
-    const bool refill = it + 2 < n_tiles;
-    if (refill) stage_load(it + 2);
-    nxt = kTileDead;
-    if (it + 1 < n_tiles) {
-      nxt = tclass(it + 1);
-      if (nxt != kTileDead) mma_s(smem[stage ^ 1][0], n0, n1);
+        for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+          for (int db = 0; db < 2; ++db) o[db] = mfma32(vop[sb][kc][db], pop[sb][kc], o[db]);
     }
-    if (cur != kTileDead) soft_pv(it, cur, c0, c1, smem[stage][1]);
-    if (refill) {
-      __syncthreads();  // every wave is done with this stage's V
-      stage_store(stage);
-    }
-    __syncthreads();
-  };
-  for (int it = 0; it < n_tiles; it += 2) {
-    step(it, ca, sa0, sa1, cb, sb0, sb1);
-    if (it + 1 >= n_tiles) break;
-    step(it + 1, cb, sb0, sb1, ca, sa0, sa1);
+    // Tile it+1 complete (the loads of it+2 may stay in flight), and every
+    // wave is done reading stage `cur` before it is refilled.
+    if (pf)
+      vm_wait_barrier<4>();
+    else
+      vm_wait_barrier<0>();
+    cur = cur == 2 ? 0 : cur + 1;
   }
 
   const float ltot = sum_xor32(lsum);
@@ -404,20 +408,20 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_pipe_kernel(FwdArgs a) 
 #pragma unroll
   for (int db = 0; db < 2; ++db)
 #pragma unroll
-    for (int rg = 0; rg < 4; ++rg)
-      *reinterpret_cast<bf16x4*>(op + 32 * db + 8 * rg + 4 * g) =
-          to_bf16x4(o[db][4 * rg] * inv, o[db][4 * rg + 1] * inv, o[db][4 * rg + 2] * inv,
-                    o[db][4 * rg + 3] * inv);
+    for (int rg4 = 0; rg4 < 4; ++rg4)
+      *reinterpret_cast<bf16x4*>(op + 32 * db + 8 * rg4 + 4 * g) =
+          to_bf16x4(o[db][4 * rg4] * inv, o[db][4 * rg4 + 1] * inv, o[db][4 * rg4 + 2] * inv,
+                    o[db][4 * rg4 + 3] * inv);
   if (g == 0) a.lse[(int64_t)bo.bh * 2 * a.n + myq] = (m + fast_log2(ltot)) * kLn2;
 }
 
 }  // namespace
 
-#ifndef BD3_FWD_PIPE
-#define BD3_FWD_PIPE 0
+#ifndef BD3_FWD_DMA
+#define BD3_FWD_DMA 1
 #endif
-#ifndef BD3_FWD_PIPE_OCC
-#define BD3_FWD_PIPE_OCC 2
+#ifndef BD3_FWD_DMA_OCC
+#define BD3_FWD_DMA_OCC 3
 #endif
 #ifndef BD3_FWD_NW
 #define BD3_FWD_NW 4
@@ -433,13 +437,13 @@ hipError_t launch_attn_fwd(const FwdArgs& a, hipStream_t stream) {
   constexpr int kNW = BD3_FWD_NW, kRB = BD3_FWD_RB, kOcc = BD3_FWD_OCC;
   constexpr int kBM = 32 * kNW * kRB;
   static_assert(128 % kBM == 0 || kBM % 128 == 0, "tile must align with n % 128 == 0");
-  if (BD3_FWD_PIPE && a.n % (32 * kNW) == 0) {
-    hipLaunchKernelGGL((attn_fwd_pipe_kernel<kNW, BD3_FWD_PIPE_OCC>), dim3(a.bh * (2 * a.n / (32 * kNW))),
-                       dim3(kNW * 64), 0, stream, a);
+  if (BD3_FWD_DMA) {  // n % 128 == 0 always holds (validated)
+    hipLaunchKernelGGL((attn_fwd_dma_kernel<BD3_FWD_DMA_OCC>), dim3(a.bh * (2 * a.n / 128)), dim3(256), 0,
+                       stream, a);
   } else if (a.n % kBM == 0) {
     hipLaunchKernelGGL((attn_fwd_kernel<kNW, kRB, kOcc>), dim3(a.bh * (2 * a.n / kBM)), dim3(kNW * 64), 0,
                        stream, a);
-  } else {  // n % 128 == 0 always holds (validated): 4 waves x 32 rows
+  } else {  // 4 waves x 32 rows
     hipLaunchKernelGGL((attn_fwd_kernel<4, 1, 2>), dim3(a.bh * (2 * a.n / 128)), dim3(256), 0, stream, a);
   }
   return hipGetLastError();

@@ -96,6 +96,18 @@ __device__ __forceinline__ float shfl_xor(float x, int m) {
 // wave index, tile counts derived from blockIdx): moving it to an SGPR lets
 // the compiler branch on it with scalar branches instead of exec masks.
 __device__ __forceinline__ int wave_uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ __forceinline__ uint32_t wave_uniform_u32(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_readfirstlane((int)x);
+}
+// A wave-uniform pointer moved to SGPRs, so address arithmetic on it stays
+// scalar. readfirstlane returns int: each half goes through uint32_t so the
+// low half is zero-extended (a sign-extended low half would corrupt the high).
+template <typename T>
+__device__ __forceinline__ T* uniform_ptr(T* p) {
+  const uint64_t b = (uint64_t)(uintptr_t)p;
+  const uint64_t u = (uint64_t)wave_uniform_u32((uint32_t)b) | ((uint64_t)wave_uniform_u32((uint32_t)(b >> 32)) << 32);
+  return (T*)(uintptr_t)u;
+}
 
 // Waits for every outstanding vector-memory load of this wave. Placed after
 // the prologue loads so that no load is still pending on any path into a

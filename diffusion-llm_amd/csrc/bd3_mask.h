@@ -144,19 +144,21 @@ BD3_HD RowGroup train_row_group(int q0, int R, int n, int bs) {
   return g;
 }
 
+// Written with non-short-circuit operators so that, with a wave-uniform
+// RowGroup, the device code is a few scalar compares and selects, no branches.
 BD3_HD int row_group_class(const RowGroup& g, int k0, int C, int n) {
   const bool kc = k0 >= n;
   const int a = kc ? k0 - n : k0;  // key offset inside its half
   const int e = a + C;
-  if (!kc) {
-    if (g.clean) return kNone;  // clean rows never see noisy keys
-    if (e <= g.diag_lo || a >= g.diag_hi) return kNone;
-    if (g.one_block && g.diag_lo <= a && e <= g.diag_hi) return kFull;
-    return kPartial;
-  }
-  if (a >= g.live_end) return kNone;
-  if (e <= g.full_end) return kFull;
-  return kPartial;
+  // noisy keys: clean rows never see them; noisy rows see their own blocks
+  const bool nz_dead = (g.clean != 0) | (e <= g.diag_lo) | (a >= g.diag_hi);
+  const bool nz_full = (g.one_block != 0) & (g.diag_lo <= a) & (e <= g.diag_hi);
+  // clean keys: a prefix seen by every row, then a partial band
+  const bool cl_dead = a >= g.live_end;
+  const bool cl_full = e <= g.full_end;
+  const bool dead = kc ? cl_dead : nz_dead;
+  const bool full = kc ? cl_full : nz_full;
+  return dead ? kNone : (full ? kFull : kPartial);
 }
 
 BD3_HD int train_class(int q0, int R, int k0, int C, int n, int bs) {
@@ -192,22 +194,82 @@ BD3_HD KeyGroup train_key_group(int k0, int C, int n, int bs) {
   return g;
 }
 
+// Branch-free like row_group_class.
 BD3_HD int key_group_class(const KeyGroup& g, int q0, int R, int n) {
   const bool qc = q0 >= n;
   const int r = qc ? q0 - n : q0;  // row offset inside its half
   const int e = r + R;
-  if (!g.clean) {
-    if (qc) return kNone;  // clean rows never see noisy keys
-    if (e <= g.noisy_lo || r >= g.noisy_hi) return kNone;
-    if (g.one_block && g.noisy_lo <= r && e <= g.noisy_hi) return kFull;
-    return kPartial;
-  }
+  // noisy keys: clean rows never see them; noisy rows of the same blocks do
+  const bool nz_dead = qc | (e <= g.noisy_lo) | (r >= g.noisy_hi);
+  const bool nz_full = (g.one_block != 0) & (g.noisy_lo <= r) & (e <= g.noisy_hi);
+  // clean keys: rows from live_lo on see some key, from full_lo on all keys
   const int live_lo = qc ? g.cl_live_lo : g.nz_live_lo;
   const int full_lo = qc ? g.cl_full_lo : g.nz_full_lo;
   const int row_end = qc ? e : imin(e, n);
-  if (row_end <= live_lo || (!qc && r >= n)) return kNone;
-  if (r >= full_lo) return kFull;
-  return kPartial;
+  const bool cl_dead = (row_end <= live_lo) | (!qc & (r >= n));
+  const bool cl_full = r >= full_lo;
+  const bool dead = g.clean ? cl_dead : nz_dead;
+  const bool full = g.clean ? cl_full : nz_full;
+  return dead ? kNone : (full ? kFull : kPartial);
+}
+
+// The classes of one fixed group (rows for RowGroup, keys for KeyGroup)
+// against blocks [p, p+C) of the other axis, as thresholds in absolute
+// positions per half (index 0: p < n, 1: p >= n). A block inside one half is
+// dead unless p + C > lo and p < hi, and otherwise full iff p >= flo and
+// p + C <= fhi. Same answers as row_group_class / key_group_class for that
+// group (checked against the mask on the host), at a few scalar compares per
+// block once the bounds are in registers.
+struct ClassBounds {
+  int lo[2], hi[2], flo[2], fhi[2];
+};
+
+constexpr int kBoundBig = 1 << 30;
+
+BD3_HD ClassBounds row_group_bounds(const RowGroup& g, int n) {
+  ClassBounds b;
+  // noisy keys: clean rows see none; noisy rows see their own blocks
+  b.lo[0] = g.clean ? kBoundBig : g.diag_lo;
+  b.hi[0] = g.diag_hi;
+  b.flo[0] = g.one_block ? g.diag_lo : kBoundBig;
+  b.fhi[0] = g.diag_hi;
+  // clean keys: offsets [0, full_end) seen by all rows, none from live_end
+  b.lo[1] = 0;
+  b.hi[1] = n + g.live_end;
+  b.flo[1] = 0;
+  b.fhi[1] = n + g.full_end;
+  return b;
+}
+
+BD3_HD ClassBounds key_group_bounds(const KeyGroup& g, int n) {
+  ClassBounds b;
+  if (!g.clean) {  // noisy keys: seen by the noisy rows of their own blocks only
+    b.lo[0] = g.noisy_lo;
+    b.hi[0] = g.noisy_hi;
+    b.flo[0] = g.one_block ? g.noisy_lo : kBoundBig;
+    b.fhi[0] = g.noisy_hi;
+    b.lo[1] = kBoundBig;
+    b.hi[1] = 2 * n;
+    b.flo[1] = kBoundBig;
+    b.fhi[1] = 2 * n;
+  } else {  // clean keys: noisy rows of later blocks, clean rows of this and later blocks
+    b.lo[0] = g.nz_live_lo >= n ? kBoundBig : g.nz_live_lo;
+    b.hi[0] = n;
+    b.flo[0] = g.nz_full_lo;
+    b.fhi[0] = n;
+    b.lo[1] = n + g.cl_live_lo;
+    b.hi[1] = 2 * n;
+    b.flo[1] = n + g.cl_full_lo;
+    b.fhi[1] = 2 * n;
+  }
+  return b;
+}
+
+BD3_HD int bounds_class(const ClassBounds& b, int p, int C, int n) {
+  const int h = p >= n;
+  const bool live = (p + C > b.lo[h]) & (p < b.hi[h]);
+  const bool full = (p >= b.flo[h]) & (p + C <= b.fhi[h]);
+  return live ? (full ? kFull : kPartial) : kNone;
 }
 
 // Key ranges (in key-tile units of `tile` keys) a training row group

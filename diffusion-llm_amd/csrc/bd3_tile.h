@@ -92,6 +92,18 @@ __device__ __forceinline__ KeyGroup uniform_key_group(int k0, int C, int n, int 
   return g;
 }
 
+// Class thresholds moved to SGPRs (they are the same for the whole wave).
+__device__ __forceinline__ ClassBounds uniform_bounds(ClassBounds b) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    b.lo[h] = wave_uniform(b.lo[h]);
+    b.hi[h] = wave_uniform(b.hi[h]);
+    b.flo[h] = wave_uniform(b.flo[h]);
+    b.fhi[h] = wave_uniform(b.fhi[h]);
+  }
+  return b;
+}
+
 // Sum of the 8 bf16 values of a P operand added to acc, as 4 v_dot2c_f32_bf16
 // against (1, 1): the softmax denominator accumulates exactly the rounded
 // probabilities the PV product uses, at half the VALU cost of fp32 adds.

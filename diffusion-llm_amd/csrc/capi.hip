@@ -336,13 +336,18 @@ int bd3_mask_dump(uint8_t* out, int32_t mode, int32_t rows, int32_t kv_len, int3
 int bd3_train_classify(int32_t n, int32_t block_size, int32_t q0, int32_t k0) {
   if (n < 32 || n % 32 != 0 || block_size < 1) return -1;
   if (q0 < 0 || k0 < 0 || q0 + 32 > 2 * n || k0 + 32 > 2 * n || q0 % 32 || k0 % 32) return -1;
-  return bd3::train_class(q0, 32, k0, 32, n, block_size);
+  const bd3::RowGroup g = bd3::train_row_group(q0, 32, n, block_size);
+  const int c = bd3::row_group_class(g, k0, 32, n);
+  // The kernels' threshold form must give the same class.
+  return bd3::bounds_class(bd3::row_group_bounds(g, n), k0, 32, n) == c ? c : -2;
 }
 
 int bd3_train_classify_keys(int32_t n, int32_t block_size, int32_t q0, int32_t k0) {
   if (n < 32 || n % 32 != 0 || block_size < 1) return -1;
   if (q0 < 0 || k0 < 0 || q0 + 32 > 2 * n || k0 + 32 > 2 * n || q0 % 32 || k0 % 32) return -1;
-  return bd3::key_group_class(bd3::train_key_group(k0, 32, n, block_size), q0, 32, n);
+  const bd3::KeyGroup g = bd3::train_key_group(k0, 32, n, block_size);
+  const int c = bd3::key_group_class(g, q0, 32, n);
+  return bd3::bounds_class(bd3::key_group_bounds(g, n), q0, 32, n) == c ? c : -2;
 }
 
 int bd3_train_intervals(int32_t n, int32_t block_size, int32_t index, int32_t mode, int32_t* out) {

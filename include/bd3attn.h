@@ -210,13 +210,16 @@ int bd3_train_tile_census(int32_t n, int32_t block_size, int64_t* out);
 /*
  * Host-only: classification the device code uses for a 32-row query group
  * starting at q0 and a 32-key sub-block starting at k0 in training mode:
- * 0 = no live pair, 1 = every pair live, 2 = partial. For CPU tests.
+ * 0 = no live pair, 1 = every pair live, 2 = partial. For CPU tests. The
+ * class is computed both from the row group's bounds and from the
+ * per-tile threshold form the kernels keep in registers; -2 if they differ.
  */
 int bd3_train_classify(int32_t n, int32_t block_size, int32_t q0, int32_t k0);
 
 /*
  * Host-only: the same classification computed the way the key-stationary
- * backward kernel does it (fixed 32-key group at k0, 32-row group at q0).
+ * backward kernel does it (fixed 32-key group at k0, 32-row group at q0),
+ * again in both forms (-2 if they differ).
  */
 int bd3_train_classify_keys(int32_t n, int32_t block_size, int32_t q0,
                             int32_t k0);
