@@ -247,7 +247,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_kernel(FwdArgs a) {
 //   * one wave-uniform class per 64-key tile (dead / full / partial): a full
 //     tile runs straight-line code with no mask arithmetic.
 // Numerics are those of attn_fwd_kernel (same products, same lazy rescale).
-template <int OCC>
+template <int OCC, bool MASK16>
 __global__ __launch_bounds__(256, OCC) void attn_fwd_dma_kernel(FwdArgs a) {
   constexpr int kBM = 128;  // query rows per workgroup: 4 waves x 32
   constexpr int kStages = 3;
@@ -351,14 +351,25 @@ __global__ __launch_bounds__(256, OCC) void attn_fwd_dma_kernel(FwdArgs a) {
 #pragma unroll
           for (int db = 0; db < 2; ++db) vop[sb][kc][db] = sw_tr_op(vs, 32 * sb + 16 * kc, 32 * db, lane);
 
+      // Partial tile: invisible pairs to -inf. With MASK16 (block size a
+      // multiple of 16) the mask is constant on 1-row x 16-key strips:
+      // registers 0-7 of a key block hold its keys 0-15, registers 8-15 keys
+      // 16-31, so one test per strip decides them.
       if (cls == kPartial) {
 #pragma unroll
-        for (int sb = 0; sb < 2; ++sb)
+        for (int sb = 0; sb < 2; ++sb) {
+          if (MASK16) {
+            const bool lo = iv_has(riv, k0 + 32 * sb), hi = iv_has(riv, k0 + 32 * sb + 16);
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = k0 + 32 * sb + 8 * (r >> 2) + 4 * g + (r & 3);
-            s[sb][r] = iv_has(riv, key) ? s[sb][r] : -INFINITY;
+            for (int r = 0; r < 16; ++r) s[sb][r] = (r < 8 ? lo : hi) ? s[sb][r] : -INFINITY;
+          } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int key = k0 + 32 * sb + 8 * (r >> 2) + 4 * g + (r & 3);
+              s[sb][r] = iv_has(riv, key) ? s[sb][r] : -INFINITY;
+            }
           }
+        }
       }
       float mx = fmaxf(s[0][0], s[1][0]);
 #pragma unroll
@@ -438,8 +449,12 @@ hipError_t launch_attn_fwd(const FwdArgs& a, hipStream_t stream) {
   constexpr int kBM = 32 * kNW * kRB;
   static_assert(128 % kBM == 0 || kBM % 128 == 0, "tile must align with n % 128 == 0");
   if (BD3_FWD_DMA) {  // n % 128 == 0 always holds (validated)
-    hipLaunchKernelGGL((attn_fwd_dma_kernel<BD3_FWD_DMA_OCC>), dim3(a.bh * (2 * a.n / 128)), dim3(256), 0,
-                       stream, a);
+    if (a.bs % 16 == 0)
+      hipLaunchKernelGGL((attn_fwd_dma_kernel<BD3_FWD_DMA_OCC, true>), dim3(a.bh * (2 * a.n / 128)), dim3(256), 0,
+                         stream, a);
+    else
+      hipLaunchKernelGGL((attn_fwd_dma_kernel<BD3_FWD_DMA_OCC, false>), dim3(a.bh * (2 * a.n / 128)), dim3(256),
+                         0, stream, a);
   } else if (a.n % kBM == 0) {
     hipLaunchKernelGGL((attn_fwd_kernel<kNW, kRB, kOcc>), dim3(a.bh * (2 * a.n / kBM)), dim3(kNW * 64), 0,
                        stream, a);
