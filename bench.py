@@ -4,7 +4,9 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 
 Headline: one step = BD3-LM training attention
-forward + backward (bd3_attn_fwd then bd3_attn_bwd through the C ABI) at
+forward + backward (bd3_attn_fwd, bd3_attn_bwd_dq, bd3_attn_bwd_dkdv through
+the C ABI, replayed from one captured HIP graph; --eager launches them one by
+one) at
 B=8, L=1024 (sequence 2048), H=12, d=64, block 16, bf16, q/k/v/dO ~ N(0,1)
 from seed 0, resident in HBM. value = useful fwd+bwd FLOPs per second:
 3.5 x 4*d*B*H*(n^2 + n*bs) (the reference's convention,
@@ -12,8 +14,8 @@ bench/attention_bench.py:89,99, restricted to unmasked pairs).
 
 Printed on stdout as ONE JSON line, with:
   roofline      the dominant kernel's useful TFLOP/s against bf16 dense MFMA
-                peak (events on the launch stream, averaged over the timed
-                steps); traffic = its HBM bytes per launch from the committed
+                peak (HIP events on the launch stream around back-to-back
+                launches of that kernel); traffic = its HBM bytes per launch from the committed
                 rocprofv3 FETCH_SIZE / WRITE_SIZE summary
                 (profiles/hbm_traffic_pmc.md);
   cpu_baseline  the fp32 eager oracle's fwd+bwd on the host cores over a
@@ -126,30 +128,67 @@ class TrainStep:
         return 3.5 * useful_fwd_flops(self.B, self.H, self.n, self.bs)
 
 
-def time_train(step: TrainStep, steps: int, warmup: int):
+def _capture_step(step: TrainStep):
+    """One training step (forward, dQ, dK/dV launches) captured as a HIP
+    graph on a side stream. Returns the graph, or None when capture is not
+    available; the caller then launches the kernels eagerly."""
+    import torch
+    try:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        saved = step.stream
+        with torch.cuda.stream(side):
+            step.stream = torch.cuda.current_stream().cuda_stream
+            step.fwd()
+            step.bwd()
+            torch.cuda.synchronize()
+            with torch.cuda.graph(graph, stream=side):
+                step.fwd()
+                step.bwd()
+        step.stream = saved
+        torch.cuda.synchronize()
+        return graph
+    except Exception as exc:  # capture unsupported: eager launches
+        log(f"graph capture unavailable ({exc}); timing eager launches")
+        step.stream = saved
+        torch.cuda.synchronize()
+        return None
+
+
+def time_train(step: TrainStep, steps: int, warmup: int, use_graph: bool = True):
     """Warm up, then time exactly `steps` fwd+bwd steps: wall clock between
-    two synchronisations, plus HIP events around each of the step's three
-    launches (forward, dQ, dK/dV) on the stream the kernels run on.
-    Returns (ms per step, ms per launch of each kernel)."""
+    two synchronisations, each step being the forward, dQ and dK/dV launches
+    replayed from one captured HIP graph (or launched eagerly). Separately,
+    each kernel's launch duration: HIP events on the launch stream around
+    `steps` back-to-back launches of that kernel alone.
+    Returns (ms per step, ms per launch of each kernel, launch mode)."""
     import torch
     for _ in range(warmup):
         step.fwd()
         step.bwd()
     torch.cuda.synchronize()
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+    graph = _capture_step(step) if use_graph else None
+    run = graph.replay if graph is not None else (lambda: (step.fwd(), step.bwd()))
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for e in ev:
-        e[0].record()
-        step.fwd()
-        e[1].record()
-        step.bwd_dq()
-        e[2].record()
-        step.bwd_dkdv()
-        e[3].record()
+    for _ in range(steps):
+        run()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    per = [sum(e[i].elapsed_time(e[i + 1]) for e in ev) / steps for i in range(3)]
-    return wall * 1e3 / steps, {"fwd": per[0], "bwd_dq": per[1], "bwd_dkdv": per[2]}
+    per = {}
+    for name, fn in (("fwd", step.fwd), ("bwd_dq", step.bwd_dq), ("bwd_dkdv", step.bwd_dkdv)):
+        fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        per[name] = e0.elapsed_time(e1) / steps
+    return wall * 1e3 / steps, per, ("hip_graph" if graph is not None else "eager")
 
 
 def cpu_baseline(B, H, n, bs, budget_s: float):
@@ -242,7 +281,7 @@ def decode_bench(device, reps: int):
     }
 
 
-def sweep_bench(device, steps: int):
+def sweep_bench(device, steps: int, use_graph: bool = True):
     """B=4, L=2048, H=16, block sizes {4, 16, 64, 256}."""
     import torch
     from kernels._native import lib
@@ -250,9 +289,9 @@ def sweep_bench(device, steps: int):
     census = (ctypes.c_int64 * 6)()
     for bs in (4, 16, 64, 256):
         st = TrainStep(4, 16, 2048, bs, device)
-        ms, per = time_train(st, steps, 2)
+        ms, per, launch = time_train(st, steps, 2, use_graph)
         lib().bd3_train_tile_census(2048, bs, census)
-        out.append({"block_size": bs, "ms": ms, "kernel_ms": per,
+        out.append({"block_size": bs, "ms": ms, "launch": launch, "kernel_ms": per,
                     "useful_tflops": st.useful_flops() / (ms * 1e-3) / 1e12,
                     "frac_of_peak": st.useful_flops() / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
                     "useful_fraction_of_executed": census[0] / census[1]})
@@ -270,6 +309,7 @@ def main(argv=None) -> int:
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--eager", action="store_true", help="time eager launches instead of a captured HIP graph")
     args = ap.parse_args(argv)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -286,9 +326,9 @@ def main(argv=None) -> int:
 
     B, H, n, bs = 8, 12, 1024, 16
     step = TrainStep(B, H, n, bs, device)
-    ms, per = time_train(step, args.steps, args.warmup)
+    ms, per, launch = time_train(step, args.steps, args.warmup, use_graph=not args.eager)
     tflops = step.useful_flops() / (ms * 1e-3) / 1e12
-    log(f"config1 fwd+bwd: {ms * 1e3:.1f} us/step (fwd {per['fwd'] * 1e3:.1f} us, "
+    log(f"config1 fwd+bwd ({launch}): {ms * 1e3:.1f} us/step (fwd {per['fwd'] * 1e3:.1f} us, "
         f"dQ {per['bwd_dq'] * 1e3:.1f} us, dK/dV {per['bwd_dkdv'] * 1e3:.1f} us) -> {tflops:.1f} useful TFLOP/s")
 
     # Algorithmic FLOPs per launch: 2*d per live pair per matrix product the
@@ -320,6 +360,7 @@ def main(argv=None) -> int:
         "data": "synthetic: q, k, v, dO ~ N(0,1) from seed 0, bf16, resident in HBM",
         "config": {"workload": "BD3-LM training attention fwd+bwd (configs[1])", "batch": B,
                    "seq_len": n, "attn_seq": 2 * n, "heads": H, "head_dim": D, "block_size": bs},
+        "launch": launch,
         "kernel_ms": per,
         "kernel_tflops": {k: f / (t * 1e-3) / 1e12 for k, (f, t) in kernels.items()},
         "useful_fraction_of_executed": census[0] / census[1],
@@ -335,7 +376,7 @@ def main(argv=None) -> int:
         for r in result["decode"]["rows"]:
             log(f"decode n_splits={r['n_splits']:3d} ({r['rule']}): {r['us']:.1f} us, {r['GB_s']:.0f} GB/s")
     if not args.no_sweep:
-        result["sweep"] = sweep_bench(device, steps=10)
+        result["sweep"] = sweep_bench(device, steps=10, use_graph=not args.eager)
         for r in result["sweep"]:
             log(f"sweep bs={r['block_size']:3d}: {r['ms'] * 1e3:.1f} us, {r['useful_tflops']:.1f} TFLOP/s")
     if not args.no_cpu_baseline:

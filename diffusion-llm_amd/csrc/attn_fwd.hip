@@ -5,22 +5,25 @@
 // Counterpart of block_sparse_attention_fwd_kern
 // (kernels/BlockSparseFlashAttention.py:75-172).
 //
-// Work split: one workgroup per (batch*head, 64*NW-row query tile), NW waves
-// of 64 rows (two 32-row blocks) each; a query tile lies in one half. Key
-// tiles of 64 keys are staged through padded LDS, double-buffered, and
-// visited only where the mask has live pairs for the workgroup
-// (train_key_ranges); each wave skips 32x32 (row block, key block) pairs that
-// are dead for its rows and masks only partial ones (train_class), with the
-// per-row key intervals applied branch-free.
+// Work split: one workgroup per (batch*head, 128-row query tile), 4 waves of
+// 32 rows; a query tile lies in one half. Only key tiles (64 keys) where the
+// mask has live pairs for the workgroup are visited (train_key_ranges); each
+// wave skips tiles that are dead for its rows and masks only partial ones.
+//
+// Loads: K/V tiles go global -> LDS with global_load_lds_dwordx4 into a
+// three-stage ring of swizzled tiles (bd3_swz.h), two tiles ahead: no VGPR
+// staging and no LDS store pass; each tile ends with one counted vmcnt wait
+// and a plain s_barrier (the loads of the tile after next stay in flight).
 //
 // Per wave and key tile:
 //   S^T (keys x rows) = K Q^T on v_mfma_f32_32x32x16_bf16: a lane holds one
 //   query row (lane % 32) and 16 of its keys per 32x32 block, so the softmax
-//   statistics are lane-local up to one permlane32 exchange. One K operand
-//   read from LDS feeds both row blocks.
-//   O^T (64 x rows) += V^T P^T, V^T read from the row-major LDS tile by
-//   ds_read_b64_tr_b16 (shared by both row blocks), P^T taken from the S^T
-//   registers (key order in the reduction permuted identically on both sides).
+//   statistics are lane-local up to one permlane32 exchange. All K operands
+//   of the tile are read from LDS in one batch.
+//   O^T (64 x rows) += V^T P^T, V^T read from the LDS tile by
+//   ds_read_b64_tr_b16 (requested right after the S^T products, so the reads
+//   hide behind the softmax), P^T taken from the S^T registers (key order in
+//   the reduction permuted identically on both sides).
 // Softmax in base 2 with scale*log2(e) folded into one FMA. The running max
 // is updated lazily: O and l are rescaled only when some row's max grew by
 // more than kRescale (log2 units); otherwise the stale max is kept, which
@@ -36,217 +39,9 @@ namespace {
 
 constexpr float kRescale = 8.0f;
 
-template <int NW, int RB, int OCC>
-__global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_kernel(FwdArgs a) {
-  constexpr int kThreads = NW * 64;
-  constexpr int kBM = 32 * RB * NW;
-  __shared__ __attribute__((aligned(16))) __bf16 smem[2][2][kTileElems];  // [stage][K|V]
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = wave_uniform(tid >> 6);
-  const int l32 = lane & 31;
-  const int g = lane >> 5;
-
-  // Heaviest tiles first: the last tiles of each half see the most keys.
-  const BlockOrder bo(a.bh, a.heads);
-  const int tiles_half = a.n / kBM;
-  const int t = tiles_half - 1 - (bo.rank >> 1);
-  const int q0 = ((bo.rank & 1) ? 0 : a.n) + t * kBM;
-
-  const uint16_t* qp = a.q + bo.b * a.sq.b + bo.h * a.sq.h;
-  const uint16_t* kp = a.k + bo.b * a.sk.b + bo.h * a.sk.h;
-  const uint16_t* vp = a.v + bo.b * a.sv.b + bo.h * a.sv.h;
-
-  const int qrow0 = q0 + 32 * RB * wave;
-  bf16x8 qreg[RB][4];
-  RowIntervals riv[RB];
-  RowGroup rgs[RB];
-#pragma unroll
-  for (int qb = 0; qb < RB; ++qb) {
-    const int myq = qrow0 + 32 * qb + l32;
-    riv[qb] = train_row_intervals(myq, a.n, a.bs);
-    rgs[qb] = uniform_row_group(qrow0 + 32 * qb, 32, a.n, a.bs);
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-      qreg[qb][c] = __builtin_bit_cast(bf16x8, ld16(qp + (int64_t)myq * a.sq.s + 16 * c + 8 * g));
-  }
-
-  const KeyRanges kr = train_key_ranges(q0, kBM, a.n, a.bs, kTileRows);
-  const int t0 = wave_uniform(kr.t0), t2 = wave_uniform(kr.t2);
-  const int n_first = wave_uniform(kr.t1 - kr.t0);
-  const int n_tiles = n_first + wave_uniform(kr.t3 - kr.t2);
-  auto tile_of = [&](int i) { return i < n_first ? t0 + i : t2 + (i - n_first); };
-
-  TileStager<kThreads, 2> st;
-  {
-    const int64_t rs[2] = {a.sk.s, a.sv.s};
-    st.init(tid, rs);
-  }
-  auto stage_load = [&](int i) {
-    const int64_t k0 = (int64_t)tile_of(i) * kTileRows;
-    const uint16_t* base[2] = {kp + k0 * a.sk.s, vp + k0 * a.sv.s};
-    st.load(base);
-  };
-
-  f32x16 o[RB][2];          // O^T [row block][d block]
-  float m[RB], lsum[RB];     // reference max (log2 domain) and lane-local partial row sums
-#pragma unroll
-  for (int qb = 0; qb < RB; ++qb) {
-    o[qb][0] = f32x16{};
-    o[qb][1] = f32x16{};
-    m[qb] = -INFINITY;
-    lsum[qb] = 0.f;
-  }
-
-  // Every row group sees at least its own block, so n_tiles >= 1 and the
-  // prologue is unconditional (keeping it on every path also leaves no load
-  // pending into the loop).
-  {
-    stage_load(0);
-    __bf16* dst[2] = {smem[0][0], smem[0][1]};
-    st.store(dst);
-  }
-  __syncthreads();
-
-  for (int it = 0; it < n_tiles; ++it) {
-    const int stage = it & 1;
-    if (it + 1 < n_tiles) stage_load(it + 1);
-    const int k0 = wave_uniform(tile_of(it) * kTileRows);
-    const __bf16* ks = smem[stage][0];
-    const __bf16* vs = smem[stage][1];
-
-    int cls[RB][2];
-    int live[2] = {kNone, kNone};  // per key block: live for any row block
-#pragma unroll
-    for (int qb = 0; qb < RB; ++qb)
-#pragma unroll
-      for (int sb = 0; sb < 2; ++sb) {
-        cls[qb][sb] = row_group_class(rgs[qb], k0 + 32 * sb, 32, a.n);
-        live[sb] |= cls[qb][sb];
-      }
-
-    if ((live[0] | live[1]) != kNone) {
-      // S^T blocks; a dead (row block, key block) pair is skipped.
-      f32x16 s[RB][2];
-#pragma unroll
-      for (int sb = 0; sb < 2; ++sb) {
-#pragma unroll
-        for (int qb = 0; qb < RB; ++qb) s[qb][sb] = f32x16{};
-        if (live[sb] == kNone) continue;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const bf16x8 kop = lds_row_op(ks, 32 * sb, c, lane);
-#pragma unroll
-          for (int qb = 0; qb < RB; ++qb)
-            if (cls[qb][sb] != kNone) s[qb][sb] = mfma32(kop, qreg[qb][c], s[qb][sb]);
-        }
-      }
-
-      bf16x8 pop[RB][2][2];  // P^T operands [row block][key block][16-key step]
-#pragma unroll
-      for (int qb = 0; qb < RB; ++qb) {
-        if ((cls[qb][0] | cls[qb][1]) == kNone) continue;
-        float mx = -INFINITY;
-#pragma unroll
-        for (int sb = 0; sb < 2; ++sb) {
-          if (cls[qb][sb] == kNone) continue;
-          if (cls[qb][sb] == kPartial) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int key = k0 + 32 * sb + 8 * (r >> 2) + 4 * g + (r & 3);
-              s[qb][sb][r] = iv_has(riv[qb], key) ? s[qb][sb][r] : -INFINITY;
-            }
-          }
-#pragma unroll
-          for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[qb][sb][r], s[qb][sb][r + 1]));
-        }
-        const float mt = max_xor32(mx) * a.scale_log2;
-        // lazy rescale, decided for the whole wave
-        if (__ballot(mt > m[qb] + kRescale) != 0) {
-          const float mn = fmaxf(m[qb], mt);
-          const float alpha = (mn == -INFINITY) ? 1.f : fast_exp2(m[qb] - mn);
-          m[qb] = mn;
-          lsum[qb] *= alpha;
-#pragma unroll
-          for (int db = 0; db < 2; ++db)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) o[qb][db][r] *= alpha;
-        }
-        const float mu = (m[qb] == -INFINITY) ? 0.f : m[qb];
-#pragma unroll
-        for (int sb = 0; sb < 2; ++sb) {
-          if (cls[qb][sb] == kNone) continue;
-          float p[16];
-#pragma unroll
-          for (int r = 0; r < 16; ++r) p[r] = fast_exp2(fmaf(s[qb][sb][r], a.scale_log2, -mu));
-#pragma unroll
-          for (int kc = 0; kc < 2; ++kc) {
-            pop[qb][sb][kc] = to_bf16x8(p[8 * kc], p[8 * kc + 1], p[8 * kc + 2], p[8 * kc + 3],
-                                        p[8 * kc + 4], p[8 * kc + 5], p[8 * kc + 6], p[8 * kc + 7]);
-            lsum[qb] = sum_bf16x8(pop[qb][sb][kc], lsum[qb]);
-          }
-        }
-      }
-
-      // O^T += V^T P^T, each V^T operand shared by both row blocks.
-#pragma unroll
-      for (int sb = 0; sb < 2; ++sb) {
-        if (live[sb] == kNone) continue;
-#pragma unroll
-        for (int kc = 0; kc < 2; ++kc)
-#pragma unroll
-          for (int db = 0; db < 2; ++db) {
-            const bf16x8 vt = lds_tr_op(vs, 32 * sb + 16 * kc, 32 * db, lane);
-#pragma unroll
-            for (int qb = 0; qb < RB; ++qb)
-              if (cls[qb][sb] != kNone) o[qb][db] = mfma32(vt, pop[qb][sb][kc], o[qb][db]);
-          }
-      }
-    }
-
-    if (it + 1 < n_tiles) {
-      __bf16* dst[2] = {smem[stage ^ 1][0], smem[stage ^ 1][1]};
-      st.store(dst);
-    }
-    __syncthreads();
-  }
-
-  // Epilogue: O = O^T / l, lse = (m + log2 l) * ln 2.
-  uint16_t* op = a.o + bo.b * a.so.b + bo.h * a.so.h;
-#pragma unroll
-  for (int qb = 0; qb < RB; ++qb) {
-    const int myq = qrow0 + 32 * qb + l32;
-    const float ltot = sum_xor32(lsum[qb]);
-    const float inv = 1.f / ltot;
-#pragma unroll
-    for (int db = 0; db < 2; ++db)
-#pragma unroll
-      for (int rg = 0; rg < 4; ++rg) {
-        const int d = 32 * db + 8 * rg + 4 * g;
-        *reinterpret_cast<bf16x4*>(op + (int64_t)myq * a.so.s + d) =
-            to_bf16x4(o[qb][db][4 * rg] * inv, o[qb][db][4 * rg + 1] * inv,
-                      o[qb][db][4 * rg + 2] * inv, o[qb][db][4 * rg + 3] * inv);
-      }
-    if (g == 0) a.lse[(int64_t)bo.bh * 2 * a.n + myq] = (m[qb] + fast_log2(ltot)) * kLn2;
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Direct-load forward. The per-wave critical path of the staged kernel above
-// is mostly exposed latency (a single wave per SIMD takes as long per key
-// tile as three), so this variant shortens it:
-//   * K/V tiles go global -> LDS with global_load_lds_dwordx4 into a
-//     three-stage ring of swizzled tiles (bd3_swz.h), two tiles ahead; no
-//     VGPR staging, no LDS store pass, one counted vmcnt wait + barrier per
-//     tile (the barrier is plain s_barrier: the loads of the tile after next
-//     stay in flight across it);
-//   * all K operands of a tile are read from LDS in one batch, and the V^T
-//     operands are requested right after the S^T products are issued, so
-//     their latency hides behind the softmax;
-//   * one wave-uniform class per 64-key tile (dead / full / partial): a full
-//     tile runs straight-line code with no mask arithmetic.
-// Numerics are those of attn_fwd_kernel (same products, same lazy rescale).
+// One class per 64-key tile for the wave (dead / full / partial, from the
+// row group's thresholds): a full tile runs straight-line code with no mask
+// arithmetic. MASK16: the block size is a multiple of 16.
 template <int OCC, bool MASK16>
 __global__ __launch_bounds__(256, OCC) void attn_fwd_dma_kernel(FwdArgs a) {
   constexpr int kBM = 128;  // query rows per workgroup: 4 waves x 32
@@ -428,39 +223,17 @@ __global__ __launch_bounds__(256, OCC) void attn_fwd_dma_kernel(FwdArgs a) {
 
 }  // namespace
 
-#ifndef BD3_FWD_DMA
-#define BD3_FWD_DMA 1
-#endif
-#ifndef BD3_FWD_DMA_OCC
-#define BD3_FWD_DMA_OCC 3
-#endif
-#ifndef BD3_FWD_NW
-#define BD3_FWD_NW 4
-#endif
-#ifndef BD3_FWD_RB
-#define BD3_FWD_RB 1
-#endif
 #ifndef BD3_FWD_OCC
 #define BD3_FWD_OCC 3
 #endif
 
 hipError_t launch_attn_fwd(const FwdArgs& a, hipStream_t stream) {
-  constexpr int kNW = BD3_FWD_NW, kRB = BD3_FWD_RB, kOcc = BD3_FWD_OCC;
-  constexpr int kBM = 32 * kNW * kRB;
-  static_assert(128 % kBM == 0 || kBM % 128 == 0, "tile must align with n % 128 == 0");
-  if (BD3_FWD_DMA) {  // n % 128 == 0 always holds (validated)
-    if (a.bs % 16 == 0)
-      hipLaunchKernelGGL((attn_fwd_dma_kernel<BD3_FWD_DMA_OCC, true>), dim3(a.bh * (2 * a.n / 128)), dim3(256), 0,
-                         stream, a);
-    else
-      hipLaunchKernelGGL((attn_fwd_dma_kernel<BD3_FWD_DMA_OCC, false>), dim3(a.bh * (2 * a.n / 128)), dim3(256),
-                         0, stream, a);
-  } else if (a.n % kBM == 0) {
-    hipLaunchKernelGGL((attn_fwd_kernel<kNW, kRB, kOcc>), dim3(a.bh * (2 * a.n / kBM)), dim3(kNW * 64), 0,
-                       stream, a);
-  } else {  // 4 waves x 32 rows
-    hipLaunchKernelGGL((attn_fwd_kernel<4, 1, 2>), dim3(a.bh * (2 * a.n / 128)), dim3(256), 0, stream, a);
-  }
+  // n % 128 == 0 always holds (validated): 128-row query tiles of 4 waves.
+  const dim3 grid(a.bh * (2 * a.n / 128)), block(256);
+  if (a.bs % 16 == 0)
+    hipLaunchKernelGGL((attn_fwd_dma_kernel<BD3_FWD_OCC, true>), grid, block, 0, stream, a);
+  else
+    hipLaunchKernelGGL((attn_fwd_dma_kernel<BD3_FWD_OCC, false>), grid, block, 0, stream, a);
   return hipGetLastError();
 }
 

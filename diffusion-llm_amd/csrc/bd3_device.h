@@ -109,12 +109,6 @@ __device__ __forceinline__ T* uniform_ptr(T* p) {
   return (T*)(uintptr_t)u;
 }
 
-// Waits for every outstanding vector-memory load of this wave. Placed after
-// the prologue loads so that no load is still pending on any path into a
-// main loop; otherwise the compiler's conservative wait-count merge at the
-// loop header makes the first use of prologue registers wait on the loop's
-// own prefetch loads.
-__device__ __forceinline__ void wait_all_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // 16-byte global load/store helpers (bf16 rows are 128 B at head_dim 64).
 __device__ __forceinline__ u32x4 ld16(const void* p) {

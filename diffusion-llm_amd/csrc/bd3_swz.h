@@ -41,8 +41,8 @@ typedef __attribute__((address_space(3))) void lds_void;
 // Issued as inline assembly on purpose: the compiler cannot tell the ring
 // stages apart, so with the builtin it waits for every outstanding direct
 // load (vmcnt(0)) before the next LDS read of any stage, which serialises the
-// prefetch. The kernels instead wait explicitly (wait_all_loads or a counted
-// vmcnt) before the barrier that publishes a stage. The compiler never keeps
+// prefetch. The kernels instead wait explicitly (a counted vmcnt) before the
+// barrier that publishes a stage. The compiler never keeps
 // a value in M0 across statements on this path (it sets M0 right before each
 // of its own uses), so clobbering it here is safe.
 __device__ __forceinline__ void dma16(const void* base, uint32_t off_bytes, uint32_t lds_addr) {
@@ -81,14 +81,6 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 template <int N>
 __device__ __forceinline__ void vm_wait_barrier() {
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
-}
-
-// Per-lane byte offset of a direct load into 1 KB block `blk` of a tile,
-// relative to the block's first row: row 8*blk + lane/8 of the tile, logical
-// chunk (lane%8) ^ swz(that row). row_stride in elements.
-__device__ __forceinline__ uint32_t dma_lane_off(int lane, int blk, int row_stride) {
-  const int r = 8 * blk + (lane >> 3);
-  return (uint32_t)(2 * ((lane >> 3) * row_stride + 8 * ((lane & 7) ^ swz(r))));
 }
 
 // Row operand (A or B of a 32x32x16 MFMA whose k index runs along the tile's
