@@ -107,13 +107,12 @@ bd3::BwdArgs bwd_args(const void* q, const void* k, const void* v, const void* o
 }
 
 int32_t auto_splits(int32_t batch, int32_t heads, int32_t q_len, int32_t kv_len) {
-  // About three workgroups per CU on a 256-CU part: a whole number of
-  // workgroups per CU keeps every CU streaming until the end (at 1.5 per CU
-  // half the CUs run a second wave of workgroups alone), while more splits
-  // only add partial traffic and merge work. Never fewer than 128 keys per
-  // split. Measured at configs[3]: 2 splits 67 us + 5 us merge vs 77 us at 1.
+  // At least one workgroup per CU on a 256-CU part; beyond that more splits
+  // only add partial traffic and a merge launch. Never fewer than 128 keys
+  // per split. Measured at configs[3] (384 workgroups at one split): 66 us at
+  // one split, 68 us at two (including the merge), 71 us at three.
   const int64_t base = (int64_t)batch * heads * decode_q_tiles(q_len);
-  const int64_t target = 768;
+  const int64_t target = 256;
   int64_t s = (target + base - 1) / base;
   const int64_t max_by_len = kv_len / 128 > 0 ? kv_len / 128 : 1;
   if (s > max_by_len) s = max_by_len;

@@ -20,9 +20,10 @@
 //   (ds_read_b64_tr_b16) as the A operand of O^T += V^T P^T.
 // decode16_partial: the same for q_len <= 16 (a cached denoising step of one
 //   16-token block) on v_mfma_f32_16x16x32_bf16, so no MFMA row or softmax
-//   lane is spent on absent queries. Each wave double-buffers its 64-key K/V
-//   chunks in registers: the loads of chunk i+1 are in flight while chunk i is
-//   computed.
+//   lane is spent on absent queries. Waves step over 32-key chunks fetched
+//   with full-row loads into registers, staged through wave-private LDS
+//   tiles; the loads of a wave's next chunk are in flight while the current
+//   one is computed.
 // decode_combine: merges the splits, weights exp2(lse_s - max lse) (the
 //   reference's split_kv_reduce_kern arithmetic, :109-127), 4 outputs per
 //   thread.
@@ -228,43 +229,54 @@ __global__ __launch_bounds__(kThreads) void decode_partial(DecodeArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// q_len <= 16: 16-row query tile on v_mfma_f32_16x16x32_bf16.
-//   S^T block (16 keys x 16 rows) = K Q^T: A = K (lane: key 16kb + lane%16,
-//   d 32c + 8h .. +7 with h = lane/16), B = Q^T (lane: row lane%16, same d);
-//   result lane (row lane%16, h) holds keys 16kb + 4h + r.
-//   O^T (16 d x 16 rows) += V^T P^T over 32 keys: B = P^T from the S^T
-//   registers of key blocks 2t and 2t+1, A = V^T read transposed from the
-//   wave's row-major LDS tile with the same key order.
+// q_len <= 16: 16-row query tile on v_mfma_f32_16x16x32_bf16, 32-key chunks.
+//   K and V of a chunk are fetched with full-row loads (8 lanes x 16 bytes
+//   cover one 128-byte key row, so every load instruction requests 8 whole
+//   rows): measured on MI355X, half-row requests (16 keys x 64 bytes per
+//   instruction, the layout the MFMA operands want) cost 7-12% of the HBM
+//   read rate at this access pattern, and 32-key chunks (8 KB of K and V in
+//   flight per wave) stream 7% faster than 64-key chunks. Both tiles go
+//   through the wave's private row-major LDS tiles:
+//   S^T block (16 keys x 16 rows) = K Q^T: A = K read from the K tile (lane:
+//   key 16kb + lane%16, d 32c + 8h .. +7 with h = lane/16), B = Q^T (lane:
+//   row lane%16, same d); result lane (row lane%16, h) holds keys
+//   16kb + 4h + r.
+//   O^T (16 d x 16 rows) += V^T P^T over the 32 keys: B = P^T from the S^T
+//   registers of both key blocks, A = V^T read transposed from the V tile
+//   with the same key order.
 constexpr int kQ16 = 16;
+constexpr int kChunk16 = 32;                         // keys per wave step
+constexpr int kTile16 = kChunk16 * kStride;          // bf16 per K or V tile
+constexpr int kLoads16 = kChunk16 * 128 / (64 * 16);  // 16-byte loads per lane and tensor
 
+template <int NW>
 struct Merge16 {
-  float o[kNW][kHeadDim][kQ16 + 1];
-  float m[kNW][kQ16];
-  float l[kNW][kQ16];
+  float o[NW][kHeadDim][kQ16 + 1];
+  float m[NW][kQ16];
+  float l[NW][kQ16];
 };
-constexpr size_t kSmem16 = kVBytes > sizeof(Merge16) ? kVBytes : sizeof(Merge16);
+template <int NW>
+constexpr size_t smem16_bytes() {
+  return sizeof(__bf16) * NW * 2 * kTile16 > sizeof(Merge16<NW>) ? sizeof(__bf16) * NW * 2 * kTile16
+                                                                 : sizeof(Merge16<NW>);
+}
 constexpr float kRescale16 = 8.0f;
 
-struct Chunk16 {
-  u32x4 k[4][2];  // K A-operands [16-key block][32-d chunk]
-  u32x4 v[8];     // V rows: lane + 64j -> row (lane + 64j)/8, 16-byte part lane%8
-};
-
-#ifndef BD3_DEC16_DBUF
-#define BD3_DEC16_DBUF 0
-#endif
 #ifndef BD3_DEC16_OCC
 #define BD3_DEC16_OCC 4
 #endif
 
-__global__ __launch_bounds__(kThreads, BD3_DEC16_OCC) void decode16_partial(DecodeArgs a) {
-  __shared__ __attribute__((aligned(16))) char smem[kSmem16];
+template <int NW>
+__global__ __launch_bounds__(NW * 64, BD3_DEC16_OCC) void decode16_partial(DecodeArgs a) {
+  constexpr int kNT = NW * 64;
+  __shared__ __attribute__((aligned(16))) char smem[smem16_bytes<NW>()];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = wave_uniform(tid >> 6);
   const int l16 = lane & 15;
   const int hq = lane >> 4;  // 16-lane group
-  __bf16* vs = reinterpret_cast<__bf16*>(smem) + wave * kVElems;
+  __bf16* ks = reinterpret_cast<__bf16*>(smem) + wave * 2 * kTile16;
+  __bf16* vs = ks + kTile16;
 
   const int split = blockIdx.x;
   const int bh = blockIdx.z;
@@ -285,51 +297,65 @@ __global__ __launch_bounds__(kThreads, BD3_DEC16_OCC) void decode16_partial(Deco
   const int key_end = wave_uniform(decode_key_end(0, kQ16, a.q_len, a.kv_len, a.bs));
   const int lo = wave_uniform(split * a.split_len);
   const int hi = wave_uniform(imin(lo + a.split_len, key_end));
-  const int n_chunks = hi > lo ? (hi - lo + kChunk - 1) / kChunk : 0;
+  const int n_chunks = hi > lo ? (hi - lo + kChunk16 - 1) / kChunk16 : 0;
   // keys below kfull are seen by every row (row 0 has the smallest position)
   const int kfull = wave_uniform(imin(((a.kv_len - a.q_len) / a.bs + 1) * a.bs, a.kv_len));
 
-  auto load = [&](Chunk16& cb, int ch) {
-    const int c0 = lo + ch * kChunk;
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      const int key = imin(c0 + 16 * kb + l16, a.kv_len - 1);
-#pragma unroll
-      for (int c = 0; c < 2; ++c) cb.k[kb][c] = ld16_stream(kp + (int64_t)key * a.sk.s + 32 * c + 8 * hq);
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int key = imin(c0 + (lane >> 3) + 8 * j, a.kv_len - 1);
-      cb.v[j] = ld16_stream(vp + (int64_t)key * a.sv.s + 8 * (lane & 7));
-    }
-  };
-
   f32x4 o[4] = {};  // O^T [16-d block]: lane (row l16, hq) holds d 16db + 4hq + r
   float m = -INFINITY, lsum = 0.f;
+  const int tr_row = l16 >> 2;
+  const int tr_col = 4 * (lane & 3);
 
-  auto compute = [&](const Chunk16& cb, int ch) {
-    const int c0 = lo + ch * kChunk;
+  // lane + 64j -> key row c0 + lane/8 + 8j, 16-byte part lane%8
+  u32x4 kr[kLoads16], vr[kLoads16];
+  // Wave step i handles chunk (i + r0) mod n_chunks. Without the rotation every
+  // workgroup reads the same offset of its head's K/V at the same time, and the
+  // head stride (kv_len x 128 bytes) piles those reads onto few HBM channels;
+  // starting head bh at chunk 7 bh spreads them (measured 71 -> 66 us at
+  // 32 x 12 heads, kv_len 4112, one split).
+  const int r0 = wave_uniform(n_chunks > 0 ? (bh * 7) % n_chunks : 0);
+  auto rot = [&](int i) { const int c = i + r0; return c >= n_chunks ? c - n_chunks : c; };
+  auto load = [&](int ch) {
+    const int c0 = lo + rot(ch) * kChunk16;
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      *reinterpret_cast<u32x4*>(&vs[((lane >> 3) + 8 * j) * kStride + 8 * (lane & 7)]) = cb.v[j];
-    f32x4 s[4];
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      s[kb] = mfma16(__builtin_bit_cast(bf16x8, cb.k[kb][0]), qreg[0], f32x4{});
-      s[kb] = mfma16(__builtin_bit_cast(bf16x8, cb.k[kb][1]), qreg[1], s[kb]);
+    for (int j = 0; j < kLoads16; ++j) {
+      const int key = imin(c0 + (lane >> 3) + 8 * j, a.kv_len - 1);
+      kr[j] = ld16_stream(kp + (int64_t)key * a.sk.s + 8 * (lane & 7));
     }
-    if (c0 + kChunk > kfull || c0 + kChunk > hi) {  // partial chunk (uniform)
+#pragma unroll
+    for (int j = 0; j < kLoads16; ++j) {
+      const int key = imin(c0 + (lane >> 3) + 8 * j, a.kv_len - 1);
+      vr[j] = ld16_stream(vp + (int64_t)key * a.sv.s + 8 * (lane & 7));
+    }
+  };
+  if (wave < n_chunks) load(wave);
+  for (int ch = wave; ch < n_chunks; ch += NW) {
+    const int c0 = lo + rot(ch) * kChunk16;
+#pragma unroll
+    for (int j = 0; j < kLoads16; ++j) {
+      const int off = ((lane >> 3) + 8 * j) * kStride + 8 * (lane & 7);
+      *reinterpret_cast<u32x4*>(&ks[off]) = kr[j];
+      *reinterpret_cast<u32x4*>(&vs[off]) = vr[j];
+    }
+    // The wave's next chunk streams in while this one is computed from LDS.
+    if (ch + NW < n_chunks) load(ch + NW);
+    f32x4 s[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const __bf16* kt = &ks[(16 * kb + l16) * kStride + 8 * hq];
+      s[kb] = mfma16(*reinterpret_cast<const bf16x8*>(kt), qreg[0], f32x4{});
+      s[kb] = mfma16(*reinterpret_cast<const bf16x8*>(kt + 32), qreg[1], s[kb]);
+    }
+    if (c0 + kChunk16 > kfull || c0 + kChunk16 > hi) {  // partial chunk (uniform)
       const int lim = imin(khi, hi);
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
           s[kb][r] = (c0 + 16 * kb + 4 * hq + r < lim) ? s[kb][r] : -INFINITY;
     }
     float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
                      fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
-    mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(s[2][0], s[2][1]), fmaxf(s[2][2], s[2][3])),
-                         fmaxf(fmaxf(s[3][0], s[3][1]), fmaxf(s[3][2], s[3][3]))));
     mx = fmaxf(mx, shfl_xor(mx, 16));
     mx = max_xor32(mx);
     const float mt = mx * a.scale_log2;
@@ -342,59 +368,29 @@ __global__ __launch_bounds__(kThreads, BD3_DEC16_OCC) void decode16_partial(Deco
       for (int db = 0; db < 4; ++db) o[db] *= alpha;
     }
     const float mu = (m == -INFINITY) ? 0.f : m;
-    float p[4][4];
+    float p[2][4];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         p[kb][r] = fast_exp2(fmaf(s[kb][r], a.scale_log2, -mu));
         lsum += p[kb][r];
       }
-    const int tr_row = l16 >> 2;
-    const int tr_col = 4 * (lane & 3);
+    const bf16x8 pop = to_bf16x8(p[0][0], p[0][1], p[0][2], p[0][3], p[1][0], p[1][1], p[1][2], p[1][3]);
+    const int row = 4 * hq + tr_row;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const bf16x8 pop = to_bf16x8(p[2 * t][0], p[2 * t][1], p[2 * t][2], p[2 * t][3],
-                                   p[2 * t + 1][0], p[2 * t + 1][1], p[2 * t + 1][2], p[2 * t + 1][3]);
-      const int row = 32 * t + 4 * hq + tr_row;
-#pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const bf16x8 va = cat8(lds_read_tr(&vs[row * kStride + 16 * db + tr_col]),
-                               lds_read_tr(&vs[(row + 16) * kStride + 16 * db + tr_col]));
-        o[db] = mfma16(va, pop, o[db]);
-      }
+    for (int db = 0; db < 4; ++db) {
+      const bf16x8 va = cat8(lds_read_tr(&vs[row * kStride + 16 * db + tr_col]),
+                             lds_read_tr(&vs[(row + 16) * kStride + 16 * db + tr_col]));
+      o[db] = mfma16(va, pop, o[db]);
     }
-  };
-
-#if BD3_DEC16_DBUF
-  // Register double buffering: chunk i+1 (this wave's next) loads while chunk i computes.
-  Chunk16 ca, cb;
-  int ch = wave;
-  if (ch < n_chunks) load(ca, ch);
-  while (ch < n_chunks) {
-    const int nx = ch + kNW;
-    if (nx < n_chunks) load(cb, nx);
-    compute(ca, ch);
-    ch = nx;
-    if (ch >= n_chunks) break;
-    const int nx2 = ch + kNW;
-    if (nx2 < n_chunks) load(ca, nx2);
-    compute(cb, ch);
-    ch = nx2;
   }
-#else
-  for (int ch = wave; ch < n_chunks; ch += kNW) {
-    Chunk16 ca;
-    load(ca, ch);
-    compute(ca, ch);
-  }
-#endif
 
-  // Merge the four waves' states.
+  // Merge the waves' states.
   lsum += shfl_xor(lsum, 16);
   lsum = sum_xor32(lsum);
-  __syncthreads();  // V staging area is reused below
-  Merge16* ml = reinterpret_cast<Merge16*>(smem);
+  __syncthreads();  // the K/V tiles are reused below
+  Merge16<NW>* ml = reinterpret_cast<Merge16<NW>*>(smem);
 #pragma unroll
   for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -405,36 +401,51 @@ __global__ __launch_bounds__(kThreads, BD3_DEC16_OCC) void decode16_partial(Deco
   }
   __syncthreads();
 
-  // 256 threads x 4 outputs = 16 rows x 64 d.
-  const int row = tid >> 4, d0 = 4 * (tid & 15);
+  // kNT threads x kOut outputs = 16 rows x 64 d.
+  constexpr int kOut = kQ16 * kHeadDim / kNT;
+  constexpr int kTPR = kHeadDim / kOut;  // threads per row
+  const int row = tid / kTPR, d0 = kOut * (tid % kTPR);
   float mm = -INFINITY;
 #pragma unroll
-  for (int w = 0; w < kNW; ++w) mm = fmaxf(mm, ml->m[w][row]);
+  for (int w = 0; w < NW; ++w) mm = fmaxf(mm, ml->m[w][row]);
   const float mu = (mm == -INFINITY) ? 0.f : mm;
   float lt = 0.f;
-  f32x4 ot = {};
+  float ot[kOut] = {};
 #pragma unroll
-  for (int w = 0; w < kNW; ++w) {
+  for (int w = 0; w < NW; ++w) {
     const float wgt = fast_exp2(ml->m[w][row] - mu);
     lt += wgt * ml->l[w][row];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) ot[j] += wgt * ml->o[w][d0 + j][row];
+    for (int j = 0; j < kOut; ++j) ot[j] += wgt * ml->o[w][d0 + j][row];
   }
   if (a.n_splits == 1) {
     if (row < a.q_len) {
       const float inv = 1.f / lt;
-      *reinterpret_cast<bf16x4*>(a.o + b * a.so.b + h * a.so.h + (int64_t)row * a.so.s + d0) =
-          to_bf16x4(ot[0] * inv, ot[1] * inv, ot[2] * inv, ot[3] * inv);
+      uint16_t* dst = a.o + b * a.so.b + h * a.so.h + (int64_t)row * a.so.s + d0;
+      if constexpr (kOut == 2) {
+        const bf16x4 y = to_bf16x4(ot[0] * inv, ot[1] * inv, 0.f, 0.f);
+        *reinterpret_cast<bf16x2*>(dst) = bf16x2{y[0], y[1]};
+      } else {
+#pragma unroll
+        for (int j = 0; j < kOut; j += 4)
+          *reinterpret_cast<bf16x4*>(dst + j) =
+              to_bf16x4(ot[j] * inv, ot[j + 1] * inv, ot[j + 2] * inv, ot[j + 3] * inv);
+      }
     }
   } else {
     const int64_t slot = (int64_t)bh * a.q_tiles * a.n_splits + split;  // q_tiles == 1
     const float inv = lt > 0.f ? 1.f / lt : 0.f;
-    *reinterpret_cast<f32x4*>(&a.part_o[(slot * kQT + row) * kHeadDim + d0]) = ot * inv;
-    if ((tid & 15) == 0) a.part_lse[slot * kQT + row] = lt > 0.f ? mm + fast_log2(lt) : -INFINITY;
+    float* dst = &a.part_o[(slot * kQT + row) * kHeadDim + d0];
+#pragma unroll
+    for (int j = 0; j < kOut; ++j) dst[j] = ot[j] * inv;
+    if (tid % kTPR == 0) a.part_lse[slot * kQT + row] = lt > 0.f ? mm + fast_log2(lt) : -INFINITY;
   }
 }
 
-// Split merge: thread -> (row, 4 consecutive d); rows in passes of 16.
+// Split merge: thread -> (row, 4 consecutive d); rows in passes of 16. For
+// NS > 0 the call has exactly NS splits and all 2 NS loads of a row are issued
+// before the first use (one memory round trip); NS == 0 takes any count.
+template <int NS>
 __global__ __launch_bounds__(kThreads) void decode_combine(DecodeArgs a) {
   const int qt = blockIdx.x;
   const int bh = blockIdx.y;
@@ -447,14 +458,33 @@ __global__ __launch_bounds__(kThreads) void decode_combine(DecodeArgs a) {
   for (int pass = 0; pass < kQT / 16; ++pass) {
     const int row = pass * 16 + (threadIdx.x >> 4);
     if (i0 + row >= a.q_len) continue;
-    float mm = -INFINITY;
-    for (int s = 0; s < a.n_splits; ++s) mm = fmaxf(mm, a.part_lse[(slot0 + s) * kQT + row]);
-    float wt = 0.f;
+    const float* lp = a.part_lse + slot0 * kQT + row;                  // split s: lp[s * kQT]
+    const float* pp = a.part_o + (slot0 * kQT + row) * kHeadDim + d0;  // split s: pp[s * kQT * kHeadDim]
+    float mm = -INFINITY, wt = 0.f;
     f32x4 acc = {};
-    for (int s = 0; s < a.n_splits; ++s) {
-      const float w = fast_exp2(a.part_lse[(slot0 + s) * kQT + row] - mm);  // empty split -> 0
-      wt += w;
-      acc += w * *reinterpret_cast<const f32x4*>(&a.part_o[((slot0 + s) * kQT + row) * kHeadDim + d0]);
+    if constexpr (NS > 0) {
+      float l[NS];
+      f32x4 po[NS];
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        l[s] = lp[s * kQT];
+        po[s] = *reinterpret_cast<const f32x4*>(pp + s * kQT * kHeadDim);
+      }
+#pragma unroll
+      for (int s = 0; s < NS; ++s) mm = fmaxf(mm, l[s]);
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const float w = fast_exp2(l[s] - mm);  // empty split -> 0
+        wt += w;
+        acc += w * po[s];
+      }
+    } else {
+      for (int s = 0; s < a.n_splits; ++s) mm = fmaxf(mm, lp[s * kQT]);
+      for (int s = 0; s < a.n_splits; ++s) {
+        const float w = fast_exp2(lp[s * kQT] - mm);
+        wt += w;
+        acc += w * *reinterpret_cast<const f32x4*>(pp + s * kQT * kHeadDim);
+      }
     }
     const float inv = 1.f / wt;
     *reinterpret_cast<bf16x4*>(op + (int64_t)(i0 + row) * a.so.s + d0) =
@@ -481,12 +511,18 @@ __global__ void mask_dump_kernel(uint8_t* out, int mode, int rows, int cols, int
 hipError_t launch_decode(const DecodeArgs& a, int /*qt*/, hipStream_t stream) {
   dim3 grid(a.n_splits, a.q_tiles, a.bh);
   if (a.q_len <= kQ16)
-    hipLaunchKernelGGL(decode16_partial, grid, dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL(decode16_partial<kNW>, grid, dim3(kThreads), 0, stream, a);
   else
     hipLaunchKernelGGL(decode_partial, grid, dim3(kThreads), 0, stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.n_splits == 1) return e;
-  hipLaunchKernelGGL(decode_combine, dim3(a.q_tiles, a.bh), dim3(kThreads), 0, stream, a);
+  const dim3 cgrid(a.q_tiles, a.bh);
+  switch (a.n_splits) {
+    case 2: hipLaunchKernelGGL(decode_combine<2>, cgrid, dim3(kThreads), 0, stream, a); break;
+    case 3: hipLaunchKernelGGL(decode_combine<3>, cgrid, dim3(kThreads), 0, stream, a); break;
+    case 4: hipLaunchKernelGGL(decode_combine<4>, cgrid, dim3(kThreads), 0, stream, a); break;
+    default: hipLaunchKernelGGL(decode_combine<0>, cgrid, dim3(kThreads), 0, stream, a); break;
+  }
   return hipGetLastError();
 }
 
