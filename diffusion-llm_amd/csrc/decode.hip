@@ -6,17 +6,18 @@
 // j / bs <= (kv_len - q_len + i) / bs and j < kv_len (bd3_mask.h).
 //
 // decode_partial: one workgroup per (split, 32-row query tile, batch*head).
-//   The split's key range is cut into 64-key chunks that the four waves take
+//   The split's key range is cut into 32-key chunks that the four waves take
 //   in turn; each wave runs an online softmax over its chunks, then the four
 //   states are merged through LDS. With one split the workgroup writes O
 //   directly; otherwise it writes a normalised fp32 partial and its log2-LSE.
 //   K and V are read once per call, with non-temporal loads (ld16_stream) so
 //   the stream does not evict other data from L2 / MALL; measured 7% faster
-//   than cached loads at the configs[3] shape.
-//   S^T (32 keys x 32 rows) = K Q^T on v_mfma_f32_32x32x16_bf16 with K read
-//   from HBM straight into A-operand registers (one 16-byte load per lane and
-//   operand: a 128-byte key row is covered by 8 consecutive lanes' loads);
-//   V goes through a wave-private row-major LDS tile and is read transposed
+//   than cached loads at the configs[3] shape. Each load instruction fetches
+//   8 whole 128-byte key rows (8 lanes per row) into registers; the rows go
+//   to the wave's private row-major K and V tiles in LDS, and the loads of
+//   the wave's next chunk are issued before the current one is computed.
+//   S^T (32 keys x 32 rows) = K Q^T on v_mfma_f32_32x32x16_bf16 with K rows
+//   read from the K tile as A operands; V is read transposed
 //   (ds_read_b64_tr_b16) as the A operand of O^T += V^T P^T.
 // decode16_partial: the same for q_len <= 16 (a cached denoising step of one
 //   16-token block) on v_mfma_f32_16x16x32_bf16, so no MFMA row or softmax
@@ -37,9 +38,9 @@ namespace {
 constexpr int kNW = 4;
 constexpr int kThreads = kNW * 64;
 constexpr int kQT = 32;       // query rows per workgroup
-constexpr int kChunk = 64;    // keys per wave step
+constexpr int kSub = 32;      // keys per wave step
 constexpr int kStride = 72;   // padded LDS row (bf16)
-constexpr int kVElems = kChunk * kStride;
+constexpr int kVElems = 2 * kSub * kStride;  // a wave's K and V tiles
 
 struct MergeLds {
   float o[kNW][kHeadDim][kQT + 1];  // O^T per wave (unnormalised), padded
@@ -51,7 +52,8 @@ constexpr size_t kSmemBytes = kVBytes > sizeof(MergeLds) ? kVBytes : sizeof(Merg
 
 __global__ __launch_bounds__(kThreads) void decode_partial(DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[kSmemBytes];
-  __bf16* vs = reinterpret_cast<__bf16*>(smem) + (threadIdx.x >> 6) * kVElems;
+  __bf16* ks = reinterpret_cast<__bf16*>(smem) + (threadIdx.x >> 6) * 2 * kSub * kStride;
+  __bf16* vs = ks + kSub * kStride;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -83,67 +85,63 @@ __global__ __launch_bounds__(kThreads) void decode_partial(DecodeArgs a) {
   const int key_end = decode_key_end(i0, kQT, a.q_len, a.kv_len, a.bs);
   const int lo = split * a.split_len;
   const int hi = imin(lo + a.split_len, key_end);
-  const int n_chunks = hi > lo ? (hi - lo + kChunk - 1) / kChunk : 0;
+  const int n_chunks = hi > lo ? (hi - lo + kSub - 1) / kSub : 0;
 
   f32x16 oacc[2] = {};
   float m = -INFINITY, lsum = 0.f;
 
-  for (int ch = wave; ch < n_chunks; ch += kNW) {
-    const int c0 = lo + ch * kChunk;
-    // K A-operands for the two 32-key sub-blocks (rows clamped in-bounds).
-    bf16x8 kop[2][4];
+  // 32-key chunks, full-row loads, next chunk in flight during the compute and
+  // a per-head start rotation: the read order of decode16_partial.
+  const int r0 = n_chunks > 0 ? (bh * 7) % n_chunks : 0;
+  auto rot = [&](int i) { const int c = i + r0; return c >= n_chunks ? c - n_chunks : c; };
+  u32x4 kr[4], vr[4];  // lane + 64j -> key row c0 + lane/8 + 8j, 16-byte part lane%8
+  auto load = [&](int ch) {
+    const int c0 = lo + rot(ch) * kSub;
 #pragma unroll
-    for (int sb = 0; sb < 2; ++sb) {
-      const int key = imin(c0 + 32 * sb + l32, a.kv_len - 1);
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-        kop[sb][c] = __builtin_bit_cast(bf16x8, ld16_stream(kp + (int64_t)key * a.sk.s + 16 * c + 8 * g));
-    }
-    // V chunk -> wave-private LDS (row-major), 8 lanes per 128-byte row.
-    u32x4 vbuf[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int e = lane + 64 * j;
-      const int key = imin(c0 + (e >> 3), a.kv_len - 1);
-      vbuf[j] = ld16_stream(vp + (int64_t)key * a.sv.s + (e & 7) * 8);
+    for (int j = 0; j < 4; ++j) {
+      const int key = imin(c0 + (lane >> 3) + 8 * j, a.kv_len - 1);
+      kr[j] = ld16_stream(kp + (int64_t)key * a.sk.s + 8 * (lane & 7));
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int e = lane + 64 * j;
-      *reinterpret_cast<u32x4*>(&vs[(e >> 3) * kStride + (e & 7) * 8]) = vbuf[j];
+    for (int j = 0; j < 4; ++j) {
+      const int key = imin(c0 + (lane >> 3) + 8 * j, a.kv_len - 1);
+      vr[j] = ld16_stream(vp + (int64_t)key * a.sv.s + 8 * (lane & 7));
     }
+  };
+  if (wave < n_chunks) load(wave);
+  const int tr_row = (lane & 15) >> 2;
+  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
-    int cls[2];
-    f32x16 s[2];
+  for (int ch = wave; ch < n_chunks; ch += kNW) {
+    const int c0 = lo + rot(ch) * kSub;
 #pragma unroll
-    for (int sb = 0; sb < 2; ++sb) {
-      const int j0 = c0 + 32 * sb;
-      // keys past hi belong to the next split (or are invisible)
-      cls[sb] = j0 >= hi ? kNone : decode_class(i0, kQT, j0, 32, a.q_len, a.kv_len, a.bs);
-      if (cls[sb] == kFull && j0 + 32 > hi) cls[sb] = kPartial;
-      s[sb] = f32x16{};
-      if (cls[sb] != kNone) {
+    for (int j = 0; j < 4; ++j) {
+      const int off = ((lane >> 3) + 8 * j) * kStride + 8 * (lane & 7);
+      *reinterpret_cast<u32x4*>(&ks[off]) = kr[j];
+      *reinterpret_cast<u32x4*>(&vs[off]) = vr[j];
+    }
+    if (ch + kNW < n_chunks) load(ch + kNW);
+
+    // keys past hi belong to the next split (or are invisible)
+    int cls = c0 >= hi ? kNone : decode_class(i0, kQT, c0, kSub, a.q_len, a.kv_len, a.bs);
+    if (cls == kFull && c0 + kSub > hi) cls = kPartial;
+    if (cls == kNone) continue;
+    // S^T (32 keys x 32 rows): A = K rows from the tile (lane: key l32, d 16c + 8g .. +7).
+    f32x16 s = {};
 #pragma unroll
-        for (int c = 0; c < 4; ++c) s[sb] = mfma32(kop[sb][c], qreg[c], s[sb]);
-        if (cls[sb] == kPartial) {
+    for (int c = 0; c < 4; ++c)
+      s = mfma32(*reinterpret_cast<const bf16x8*>(&ks[l32 * kStride + 16 * c + 8 * g]), qreg[c], s);
+    if (cls == kPartial) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = j0 + 8 * (r >> 2) + 4 * g + (r & 3);
-            s[sb][r] = (key < khi && key < hi) ? s[sb][r] : -INFINITY;
-          }
-        }
-      } else {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[sb][r] = -INFINITY;
+      for (int r = 0; r < 16; ++r) {
+        const int key = c0 + 8 * (r >> 2) + 4 * g + (r & 3);
+        s[r] = (key < khi && key < hi) ? s[r] : -INFINITY;
       }
     }
-    if (cls[0] == kNone && cls[1] == kNone) continue;
 
     float mx = -INFINITY;
 #pragma unroll
-    for (int sb = 0; sb < 2; ++sb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[sb][r]);
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[r]);
     mx = max_xor32(mx);
     const float m_new = fmaxf(m, mx * a.scale_log2);
     const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
@@ -155,28 +153,22 @@ __global__ __launch_bounds__(kThreads) void decode_partial(DecodeArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
 
-    const int tr_row = (lane & 15) >> 2;
-    const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    float p[16];
 #pragma unroll
-    for (int sb = 0; sb < 2; ++sb) {
-      if (cls[sb] == kNone) continue;
-      float p[16];
+    for (int r = 0; r < 16; ++r) {
+      p[r] = fast_exp2(fmaf(s[r], a.scale_log2, -m_use));
+      lsum += p[r];
+    }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        p[r] = fast_exp2(fmaf(s[sb][r], a.scale_log2, -m_use));
-        lsum += p[r];
-      }
+    for (int kc = 0; kc < 2; ++kc) {
+      const bf16x8 pop = to_bf16x8(p[8 * kc], p[8 * kc + 1], p[8 * kc + 2], p[8 * kc + 3],
+                                   p[8 * kc + 4], p[8 * kc + 5], p[8 * kc + 6], p[8 * kc + 7]);
+      const int row = 16 * kc + 4 * g + tr_row;
 #pragma unroll
-      for (int kc = 0; kc < 2; ++kc) {
-        const bf16x8 pop = to_bf16x8(p[8 * kc], p[8 * kc + 1], p[8 * kc + 2], p[8 * kc + 3],
-                                     p[8 * kc + 4], p[8 * kc + 5], p[8 * kc + 6], p[8 * kc + 7]);
-        const int row = 32 * sb + 16 * kc + 4 * g + tr_row;
-#pragma unroll
-        for (int db = 0; db < 2; ++db) {
-          const bf16x8 va = cat8(lds_read_tr(&vs[row * kStride + 32 * db + tr_col]),
-                                 lds_read_tr(&vs[(row + 8) * kStride + 32 * db + tr_col]));
-          oacc[db] = mfma32(va, pop, oacc[db]);
-        }
+      for (int db = 0; db < 2; ++db) {
+        const bf16x8 va = cat8(lds_read_tr(&vs[row * kStride + 32 * db + tr_col]),
+                               lds_read_tr(&vs[(row + 8) * kStride + 32 * db + tr_col]));
+        oacc[db] = mfma32(va, pop, oacc[db]);
       }
     }
   }
