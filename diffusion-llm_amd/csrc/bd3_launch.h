@@ -69,10 +69,39 @@ struct DecodeArgs {
   float scale_log2;
 };
 
+struct QkvRopeArgs {
+  const uint16_t* qkv;  // (batch, seq, 3 * heads * 64), last stride 1
+  int64_t sx_b, sx_s;
+  const int64_t* positions;  // (seq) absolute positions, or null: pos0 + s
+  int pos0;
+  const float* sin_t;  // (max_pos, 32) fp32
+  const float* cos_t;
+  int max_pos;
+  uint16_t* q;
+  uint16_t* k;
+  uint16_t* v;
+  Strides3 sq, sk, sv;
+  int heads;
+  int seq;
+  int64_t total;  // batch * seq * 12 * heads work items
+};
+
+struct KvWriteArgs {
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* k_dst;
+  uint16_t* v_dst;
+  Strides3 sk, sv, skd, svd;
+  int batch, heads, seq;
+  int64_t total;  // 2 * batch * heads * seq * 8 16-byte parts
+};
+
 hipError_t launch_attn_fwd(const FwdArgs& a, hipStream_t stream);
 hipError_t launch_attn_bwd_dq(const BwdArgs& a, hipStream_t stream);
 hipError_t launch_attn_bwd_dkdv(const BwdArgs& a, hipStream_t stream);
 hipError_t launch_decode(const DecodeArgs& a, int qt, hipStream_t stream);
+hipError_t launch_qkv_rope(const QkvRopeArgs& a, hipStream_t stream);
+hipError_t launch_kv_write(const KvWriteArgs& a, hipStream_t stream);
 hipError_t launch_mask_dump(uint8_t* out, int mode, int rows, int kv_len,
                             int bs, hipStream_t stream);
 

@@ -316,6 +316,79 @@ int bd3_decode_splitkv(const void* q, const void* k, const void* v, void* o, int
                     workspace, workspace_bytes, stream);
 }
 
+int bd3_qkv_rope(const void* qkv, const int64_t* qkv_strides, int32_t batch, int32_t seq,
+                 int32_t heads, int32_t head_dim, const int64_t* positions, int32_t pos0,
+                 const float* sin_table, const float* cos_table, int32_t max_pos, void* q_out,
+                 void* k_out, void* v_out, const int64_t* out_strides, void* stream) {
+  if (batch < 1 || heads < 1 || seq < 0) return fail(BD3_EINVAL, "need batch >= 1, heads >= 1, seq >= 0");
+  if (head_dim != bd3::kHeadDim) return fail(BD3_EINVAL, "head_dim must be 64, got %d", head_dim);
+  if (qkv == nullptr || !aligned16(qkv)) return fail(BD3_EINVAL, "qkv must be a 16-byte aligned device pointer");
+  if (qkv_strides == nullptr || out_strides == nullptr) return fail(BD3_EINVAL, "strides is NULL");
+  for (int i = 0; i < 2; ++i)
+    if (qkv_strides[i] < 0 || qkv_strides[i] % 8 != 0)
+      return fail(BD3_EINVAL, "qkv stride[%d]=%lld must be a non-negative multiple of 8", i,
+                  (long long)qkv_strides[i]);
+  if (sin_table == nullptr || cos_table == nullptr || !aligned16(sin_table) || !aligned16(cos_table))
+    return fail(BD3_EINVAL, "sin_table and cos_table must be 16-byte aligned device pointers");
+  if (max_pos < 1) return fail(BD3_EINVAL, "max_pos must be >= 1");
+  if (positions == nullptr && (pos0 < 0 || (int64_t)pos0 + seq > max_pos))
+    return fail(BD3_EINVAL, "positions %d .. %lld exceed the RoPE table (max_pos %d)", pos0,
+                (long long)pos0 + seq - 1, max_pos);
+  const char* names[3] = {"q_out", "k_out", "v_out"};
+  void* outs[3] = {q_out, k_out, v_out};
+  for (int i = 0; i < 3; ++i) {
+    int st = check_tensor(outs[i], out_strides + 3 * i, names[i]);
+    if (st) return st;
+  }
+  bd3::QkvRopeArgs a;
+  a.qkv = static_cast<const uint16_t*>(qkv);
+  a.sx_b = qkv_strides[0];
+  a.sx_s = qkv_strides[1];
+  a.positions = positions;
+  a.pos0 = pos0;
+  a.sin_t = sin_table;
+  a.cos_t = cos_table;
+  a.max_pos = max_pos;
+  a.q = static_cast<uint16_t*>(q_out);
+  a.k = static_cast<uint16_t*>(k_out);
+  a.v = static_cast<uint16_t*>(v_out);
+  a.sq = s3(out_strides);
+  a.sk = s3(out_strides + 3);
+  a.sv = s3(out_strides + 6);
+  a.heads = heads;
+  a.seq = seq;
+  a.total = (int64_t)batch * seq * 12 * heads;
+  return hip_status(bd3::launch_qkv_rope(a, static_cast<hipStream_t>(stream)), "qkv_rope launch");
+}
+
+int bd3_kv_write(const void* k, const void* v, void* k_dst, void* v_dst, int32_t batch,
+                 int32_t heads, int32_t seq, int32_t head_dim, const int64_t* strides,
+                 void* stream) {
+  if (batch < 1 || heads < 1 || seq < 0) return fail(BD3_EINVAL, "need batch >= 1, heads >= 1, seq >= 0");
+  if (head_dim != bd3::kHeadDim) return fail(BD3_EINVAL, "head_dim must be 64, got %d", head_dim);
+  if (strides == nullptr) return fail(BD3_EINVAL, "strides is NULL");
+  const char* names[4] = {"k", "v", "k_dst", "v_dst"};
+  const void* ptrs[4] = {k, v, k_dst, v_dst};
+  for (int i = 0; i < 4; ++i) {
+    int st = check_tensor(ptrs[i], strides + 3 * i, names[i]);
+    if (st) return st;
+  }
+  bd3::KvWriteArgs a;
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.k_dst = static_cast<uint16_t*>(k_dst);
+  a.v_dst = static_cast<uint16_t*>(v_dst);
+  a.sk = s3(strides);
+  a.sv = s3(strides + 3);
+  a.skd = s3(strides + 6);
+  a.svd = s3(strides + 9);
+  a.batch = batch;
+  a.heads = heads;
+  a.seq = seq;
+  a.total = 2 * (int64_t)batch * heads * seq * 8;
+  return hip_status(bd3::launch_kv_write(a, static_cast<hipStream_t>(stream)), "kv_write launch");
+}
+
 int bd3_mask_dump(uint8_t* out, int32_t mode, int32_t rows, int32_t kv_len, int32_t block_size,
                   void* stream) {
   if (out == nullptr) return fail(BD3_EINVAL, "out is NULL");

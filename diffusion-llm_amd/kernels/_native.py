@@ -44,6 +44,9 @@ SIGNATURES: dict[str, tuple] = {
     "bd3_decode_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "bd3_decode_splitkv": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i32,
                                           _i32, _i64p, _f32, _c_p, _sz, _c_p]),
+    "bd3_qkv_rope": (ctypes.c_int, [_c_p, _i64p, _i32, _i32, _i32, _i32, _c_p, _i32, _c_p, _c_p, _i32,
+                                    _c_p, _c_p, _c_p, _i64p, _c_p]),
+    "bd3_kv_write": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _i32, _i32, _i32, _i32, _i64p, _c_p]),
     "bd3_mask_dump": (ctypes.c_int, [_c_p, _i32, _i32, _i32, _i32, _c_p]),
     "bd3_train_tile_census": (ctypes.c_int, [_i32, _i32, _i64p]),
     "bd3_train_classify": (ctypes.c_int, [_i32, _i32, _i32, _i32]),

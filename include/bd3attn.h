@@ -185,6 +185,48 @@ int bd3_decode_splitkv(const void* q, const void* k, const void* v, void* o,
                        void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Attention inputs of one layer in one pass: splits the fused projection
+ * into heads, applies the rotary embedding to q and k, and stores q, k and v
+ * to (batch, heads, seq, head_dim) destinations with arbitrary (b, h, s)
+ * strides -- k_out / v_out may be the slot [len, len + seq) of a
+ * preallocated KV cache, so attention reads cache and block in place.
+ * Replaces the rearrange and the two RoPE calls of
+ * BidirectionalMultiHeadAttention.forward (model/modules.py:395-407,
+ * RoPE.forward :212-240) and, with a cache, the per-step
+ * torch.cat([cache, block]) (model/modules.py:409-414).
+ *   qkv: (batch, seq, 3 * heads * head_dim) bf16, last stride 1;
+ *        qkv_strides = its (batch, seq) element strides. Column
+ *        c*heads*head_dim + h*head_dim + j is component c (0 q, 1 k, 2 v)
+ *        of head h, coordinate j (the reference's
+ *        "(three n_heads d_k)" order).
+ *   positions: device int64 (seq) absolute positions, or NULL for
+ *        pos0 .. pos0 + seq - 1 (then pos0 + seq <= max_pos is checked).
+ *        Explicit positions outside [0, max_pos) are clamped (the
+ *        reference's table lookup would raise).
+ *   sin_table, cos_table: device fp32 (max_pos, head_dim / 2), the RoPE
+ *        module's tables (sin/cos of p * theta^(-2k/head_dim)).
+ *   out_strides: 3 x 3 (b, h, s) element strides of q_out, k_out, v_out.
+ * The rotation repeats the reference's eager bf16 arithmetic (tables
+ * rounded to bf16, every product, difference and sum rounded to bf16), so
+ * outputs are bit-identical to it. seq == 0 is a no-op.
+ */
+int bd3_qkv_rope(const void* qkv, const int64_t* qkv_strides, int32_t batch, int32_t seq,
+                 int32_t heads, int32_t head_dim, const int64_t* positions, int32_t pos0,
+                 const float* sin_table, const float* cos_table, int32_t max_pos, void* q_out,
+                 void* k_out, void* v_out, const int64_t* out_strides, void* stream);
+
+/*
+ * Copies (batch, heads, seq, head_dim) bf16 k and v into k_dst / v_dst
+ * (any (b, h, s) strides; typically the slot [len, len + seq) of a
+ * preallocated cache). strides: 4 x 3 for k, v, k_dst, v_dst. Replaces the
+ * torch.cat growth of KVCache.append (model/kv_cache.py:42-55). seq == 0 is
+ * a no-op.
+ */
+int bd3_kv_write(const void* k, const void* v, void* k_dst, void* v_dst, int32_t batch,
+                 int32_t heads, int32_t seq, int32_t head_dim, const int64_t* strides,
+                 void* stream);
+
+/*
  * Writes the mask the device predicate applies, one byte per (row, key)
  * (1 = may attend), row-major:
  *   mode 0 (training): (2n, 2n) with n = rows, kv_len ignored;

@@ -154,3 +154,31 @@ def test_workspace_sizes(lib):
     assert 1 <= s <= 4112 // 128
     assert lib.bd3_decode_workspace_bytes(32, 12, 16, 4112, 64, 0) == lib.bd3_decode_workspace_bytes(
         32, 12, 16, 4112, 64, s)
+
+
+def test_qkv_rope_validation(lib):
+    xs = _i64([32 * 2304, 2304])
+    os_ = _i64([12 * 32 * 64, 32 * 64, 64] * 3)
+    call = lambda **kw: lib.bd3_qkv_rope(
+        kw.get("qkv", GOOD), kw.get("xs", xs), kw.get("batch", 2), kw.get("seq", 32), 12,
+        kw.get("d", 64), kw.get("positions", None), kw.get("pos0", 0), kw.get("sin", GOOD), GOOD,
+        kw.get("max_pos", 2048), kw.get("q", GOOD), GOOD, GOOD, kw.get("os", os_), None)
+    expect_einval(call(d=128), "head_dim must be 64")
+    expect_einval(call(batch=0), "batch >= 1")
+    expect_einval(call(seq=-1), "seq >= 0")
+    expect_einval(call(qkv=GOOD + 2), "16-byte aligned")
+    expect_einval(call(xs=_i64([32 * 2304, 2300])), "qkv stride[1]")
+    expect_einval(call(sin=None), "sin_table")
+    expect_einval(call(max_pos=0), "max_pos")
+    expect_einval(call(pos0=2040), "exceed the RoPE table")
+    expect_einval(call(pos0=-1), "exceed the RoPE table")
+    expect_einval(call(q=None), "q_out is NULL")
+    expect_einval(call(os=_i64([12 * 32 * 64, 32 * 64, 60] + [0, 0, 64] * 2)), "q_out stride[2]")
+
+
+def test_kv_write_validation(lib):
+    st = _i64([12 * 32 * 64, 32 * 64, 64] * 4)
+    expect_einval(lib.bd3_kv_write(GOOD, GOOD, GOOD, GOOD, 1, 12, 32, 32, st, None), "head_dim must be 64")
+    expect_einval(lib.bd3_kv_write(GOOD, GOOD, None, GOOD, 1, 12, 32, 64, st, None), "k_dst is NULL")
+    expect_einval(lib.bd3_kv_write(GOOD, GOOD, GOOD, GOOD, 1, 12, -2, 64, st, None), "seq >= 0")
+    expect_einval(lib.bd3_kv_write(GOOD, GOOD, GOOD, GOOD, 1, 12, 32, 64, None, None), "strides is NULL")
