@@ -23,6 +23,10 @@ Printed on stdout as ONE JSON line, with:
   decode        configs[3]: split-KV decode KV-read GB/s at splits
                 {1, 4, 8, 16}, the reference's default split rule and the
                 auto split, against 8 TB/s;
+  kv_cache      the layer's attention inputs (split + RoPE + cache
+                placement, bd3_qkv_rope) at configs[3]'s decode step and a
+                full 8 x 2048-token sequence, against the reference's eager
+                path (RoPE as bf16 ops + torch.cat of the cache);
   sweep         configs[2]: block sizes {4, 16, 64, 256} at B=4, L=2048,
                 H=16 (useful TFLOP/s and the schedule's useful fraction).
 Human-readable progress goes to stderr.
@@ -281,6 +285,83 @@ def decode_bench(device, reps: int):
     }
 
 
+def kvcache_bench(device, reps: int):
+    """Attention inputs of one layer: head split + RoPE + KV-cache placement
+    (bd3_qkv_rope) against the reference's eager path on the same GPU
+    (model/modules.py:395-414: rearrange, RoPE as bf16 tensor ops, then
+    torch.cat of the cache and the block for k and v).
+      decode_step: configs[3]'s step, 32 sequences x 12 heads, a 16-token
+        block over a 4096-token cache; ours writes q and places the block's
+        k / v in the cache slot, the reference copies the whole cache.
+      full_sequence: 8 x 2048 tokens x 12 heads (configs[1]'s shape) with no
+        cache; HBM-bound (reads the projection, writes q, k, v once).
+    `kernel_us` times the C-ABI call alone, `call_us` the Python
+    attention_inputs wrapper; HIP events, 1 GiB cache flush before each rep."""
+    import torch
+    from kernels._native import check, lib, ptr, stream_of, strides
+    from kernels.kv_cache import KVCache, attention_inputs, rope_tables
+    from perf.harness import bench
+    H, L_ = 12, lib()
+    sin, cos = rope_tables(D, 8192, device=device)
+    out = {}
+
+    def eager(qkv, kc, vc, pos0):
+        B, S, _ = qkv.shape
+        q, k, v = qkv.view(B, S, 3, H, D).permute(2, 0, 3, 1, 4)
+        pos = torch.arange(pos0, pos0 + S, device=device)
+        s_, c_ = sin[pos].to(torch.bfloat16), cos[pos].to(torch.bfloat16)
+
+        def rope(x):
+            x1, x2 = x.chunk(2, dim=-1)
+            return torch.cat([x1 * c_ - x2 * s_, x1 * s_ + x2 * c_], dim=-1)
+        q, k = rope(q), rope(k)
+        if kc is not None:
+            k, v = torch.cat([kc, k], dim=-2), torch.cat([vc, v], dim=-2)
+        return q, k, v
+
+    for name, (B, S, L) in (("decode_step", (32, 16, 4096)), ("full_sequence", (8, 2048, 0))):
+        (qkv,) = seeded_bf16((B, S, 3 * H * D), 5, 1, device)
+        q = torch.empty((B, H, S, D), device=device, dtype=torch.bfloat16)
+        kc = vc = None
+        if L:
+            kc, vc = seeded_bf16((B, H, L, D), 6, 2, device)
+            cache = KVCache.empty(1, capacity=L + S)
+            cache.append(0, kc, vc)
+            ks, vs = cache.slot(0, q, S)
+        else:
+            cache = None
+            ks, vs = torch.empty_like(q), torch.empty_like(q)
+        xs = (ctypes.c_int64 * 2)(qkv.stride(0), qkv.stride(1))
+        st = strides(q, ks, vs)
+        stream = stream_of(qkv)
+
+        def kern():
+            check(L_.bd3_qkv_rope(ptr(qkv), xs, B, S, H, D, None, L, ptr(sin), ptr(cos), sin.shape[0],
+                                  ptr(q), ptr(ks), ptr(vs), st, stream))
+
+        def call():
+            attention_inputs(qkv, H, sin, cos, L, cache, 0, False)
+
+        t_k = bench(kern, warmup=3, rep=reps, flush=True)
+        t_c = bench(call, warmup=3, rep=reps, flush=True)
+        t_e = bench(lambda: eager(qkv, kc, vc, L), warmup=3, rep=reps, flush=True)
+        nbytes = 2 * qkv.numel() * 2  # projection read once, q / k / v written once
+        row = {"batch": B, "tokens": S, "heads": H, "cache_len": L,
+               "kernel_us": t_k.median_ms * 1e3, "call_us": t_c.median_ms * 1e3,
+               "reference_eager_us": t_e.median_ms * 1e3, "algorithmic_bytes": nbytes,
+               "kernel_GB_s": nbytes / (t_k.median_ms * 1e-3) / 1e9}
+        if L:
+            row["reference_eager_bytes"] = nbytes + 2 * 2 * kc.numel() * 2  # + cat: read and write both caches
+        out[name] = row
+        del qkv, q, kc, vc, cache, ks, vs
+        torch.cuda.empty_cache()
+    full = out["full_sequence"]
+    out["roofline"] = {"bound": "hbm", "achieved": full["kernel_GB_s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                       "frac": full["kernel_GB_s"] / PEAK_HBM_GBS, "traffic": measured_traffic("qkv_rope_kernel"),
+                       "kernel": "qkv_rope_kernel (full_sequence)"}
+    return out
+
+
 def sweep_bench(device, steps: int, use_graph: bool = True):
     """B=4, L=2048, H=16, block sizes {4, 16, 64, 256}."""
     import torch
@@ -309,6 +390,7 @@ def main(argv=None) -> int:
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-kvcache", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a captured HIP graph")
     args = ap.parse_args(argv)
 
@@ -375,6 +457,12 @@ def main(argv=None) -> int:
         result["decode"] = decode_bench(device, reps=30)
         for r in result["decode"]["rows"]:
             log(f"decode n_splits={r['n_splits']:3d} ({r['rule']}): {r['us']:.1f} us, {r['GB_s']:.0f} GB/s")
+    if not args.no_kvcache:
+        result["kv_cache"] = kvcache_bench(device, reps=20)
+        for k_, r in result["kv_cache"].items():
+            if k_ != "roofline":
+                log(f"kv_cache {k_}: kernel {r['kernel_us']:.1f} us ({r['kernel_GB_s']:.0f} GB/s), "
+                    f"call {r['call_us']:.1f} us, reference eager {r['reference_eager_us']:.1f} us")
     if not args.no_sweep:
         result["sweep"] = sweep_bench(device, steps=10, use_graph=not args.eager)
         for r in result["sweep"]:

@@ -83,7 +83,7 @@ struct QkvRopeArgs {
   Strides3 sq, sk, sv;
   int heads;
   int seq;
-  int64_t total;  // batch * seq * 12 * heads work items
+  int64_t total;  // batch * seq * 4 * heads work items (< 2^31)
 };
 
 struct KvWriteArgs {

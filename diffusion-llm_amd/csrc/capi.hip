@@ -357,7 +357,9 @@ int bd3_qkv_rope(const void* qkv, const int64_t* qkv_strides, int32_t batch, int
   a.sv = s3(out_strides + 6);
   a.heads = heads;
   a.seq = seq;
-  a.total = (int64_t)batch * seq * 12 * heads;
+  a.total = (int64_t)batch * seq * 4 * heads;
+  if (a.total >= ((int64_t)1 << 31))
+    return fail(BD3_EINVAL, "batch * seq * heads too large (%lld work items, limit 2^31)", (long long)a.total);
   return hip_status(bd3::launch_qkv_rope(a, static_cast<hipStream_t>(stream)), "qkv_rope launch");
 }
 

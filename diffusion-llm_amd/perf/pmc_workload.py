@@ -10,7 +10,9 @@ Dispatches, in order and each `--reps` times:
      configs[1] (B=8, L=1024, H=12, d=64, block 16, bf16; --batch, --heads,
      --seq-len and --block-size change the shape);
   3. the split-KV decode at configs[3] (32 x 12 heads, q_len 16,
-     kv_len 4112) with the library's automatic split count.
+     kv_len 4112) with the library's automatic split count;
+  4. the layer's attention inputs (bd3_qkv_rope: head split + RoPE) over a
+     full 8 x 2048-token sequence, 12 heads.
 No timing is done here; the profiler records per-dispatch counters.
 """
 from __future__ import annotations
@@ -73,6 +75,21 @@ def main(argv=None) -> int:
                            ptr(ws), nbytes, stream_of(q)))
     torch.cuda.synchronize()
     print(f"decode done (K+V bytes per dispatch {2 * B * H * kv_len * D * 2})", flush=True)
+    del q, k, v, o, ws
+
+    import ctypes
+    from kernels.kv_cache import rope_tables
+    B, S, H = 8, 2048, 12
+    (qkv,) = seeded_bf16((B, S, 3 * H * D), 5, 1, dev)
+    sin, cos = rope_tables(D, S, device=dev)
+    qo, ko, vo = (torch.empty((B, H, S, D), device=dev, dtype=torch.bfloat16) for _ in range(3))
+    xs = (ctypes.c_int64 * 2)(qkv.stride(0), qkv.stride(1))
+    st = strides(qo, ko, vo)
+    for _ in range(args.reps):
+        check(L.bd3_qkv_rope(ptr(qkv), xs, B, S, H, D, None, 0, ptr(sin), ptr(cos), S, ptr(qo), ptr(ko),
+                             ptr(vo), st, stream_of(qkv)))
+    torch.cuda.synchronize()
+    print(f"qkv_rope done (projection bytes read per dispatch {qkv.numel() * 2})", flush=True)
     return 0
 
 

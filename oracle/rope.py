@@ -20,11 +20,12 @@ import numpy as np
 
 
 def bf16_bits(x) -> np.ndarray:
-    """float32 -> bf16 bit patterns, round to nearest even; NaN stays NaN."""
+    """float32 -> bf16 bit patterns, round to nearest even; every NaN becomes
+    the canonical quiet NaN 0x7fc0 (torch's conversion)."""
     u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
     nan = (u & np.uint32(0x7FFFFFFF)) > np.uint32(0x7F800000)
     r = (u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)
-    r = np.where(nan, (u >> np.uint32(16)) | np.uint32(0x40), r)
+    r = np.where(nan, np.uint32(0x7FC0), r)
     return r.astype(np.uint16)
 
 

@@ -171,3 +171,23 @@ def test_cache_append_api(cuda):
             kc, vc = cache.get(layer)
             assert np.array_equal(dev_bits(kc), ref.get(layer)[0])
             assert np.array_equal(dev_bits(vc), ref.get(layer)[1])
+
+
+@pytest.mark.gpu
+def test_qkv_rope_extreme_values(cuda, tables):
+    """Subnormal, huge, infinite and NaN inputs: the kernel's roundings match
+    the oracle's (and so torch's) bit for bit, including overflow to inf and
+    the canonical NaN."""
+    B, S, H = 1, 64, 4
+    rng = np.random.default_rng(21)
+    mags = np.array([1e-41, 1e-39, 3e-38, 1.0, 2.5e38, 3.3e38], dtype=np.float32)
+    x = (rng.choice(mags, (B, S, 3 * H * D)) * rng.choice([-1.0, 1.0], (B, S, 3 * H * D))).astype(np.float32)
+    x.reshape(-1)[rng.integers(0, x.size, 40)] = np.inf
+    x.reshape(-1)[rng.integers(0, x.size, 40)] = -np.inf
+    x.reshape(-1)[rng.integers(0, x.size, 40)] = np.nan
+    xb = orc.bf16_bits(x)
+    sin_d, cos_d = dev_tables(tables, cuda)
+    q, k, v = attention_inputs(bits_to_dev(xb, cuda), H, sin_d, cos_d, positions=1000)
+    qw, kw, vw = orc.attention_inputs(xb, H, *tables, positions=np.arange(1000, 1000 + S))
+    for name, got, want in (("q", q, qw), ("k", k, kw), ("v", v, vw)):
+        assert np.array_equal(dev_bits(got), want), name
