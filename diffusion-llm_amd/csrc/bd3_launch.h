@@ -96,12 +96,26 @@ struct KvWriteArgs {
   int64_t total;  // 2 * batch * heads * seq * 8 16-byte parts
 };
 
+struct SubsArgs {
+  const void* logits;  // (rows, ld) bf16 or fp32
+  int64_t ld;          // row stride in elements
+  int fp32;            // 1: fp32 logits, 0: bf16
+  const int64_t* xt;   // (rows) current tokens
+  int64_t* out;        // (rows) next tokens
+  int rows, vocab;
+  int mask_index;
+  double keep;         // s / t
+  const double* u;     // (rows, vocab) uniforms, or null: Philox4x32-10(seed, offset)
+  uint64_t seed, offset;
+};
+
 hipError_t launch_attn_fwd(const FwdArgs& a, hipStream_t stream);
 hipError_t launch_attn_bwd_dq(const BwdArgs& a, hipStream_t stream);
 hipError_t launch_attn_bwd_dkdv(const BwdArgs& a, hipStream_t stream);
 hipError_t launch_decode(const DecodeArgs& a, int qt, hipStream_t stream);
 hipError_t launch_qkv_rope(const QkvRopeArgs& a, hipStream_t stream);
 hipError_t launch_kv_write(const KvWriteArgs& a, hipStream_t stream);
+hipError_t launch_subs_sample(const SubsArgs& a, hipStream_t stream);
 hipError_t launch_mask_dump(uint8_t* out, int mode, int rows, int kv_len,
                             int bs, hipStream_t stream);
 

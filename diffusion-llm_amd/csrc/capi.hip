@@ -391,6 +391,34 @@ int bd3_kv_write(const void* k, const void* v, void* k_dst, void* v_dst, int32_t
   return hip_status(bd3::launch_kv_write(a, static_cast<hipStream_t>(stream)), "kv_write launch");
 }
 
+int bd3_subs_sample(const void* logits, int64_t ld, int32_t logits_fp32, const int64_t* xt,
+                    int64_t* out, int32_t rows, int32_t vocab, int32_t mask_index, double keep,
+                    const double* u, uint64_t seed, uint64_t offset, void* stream) {
+  if (rows < 0) return fail(BD3_EINVAL, "rows must be >= 0");
+  if (vocab < 2) return fail(BD3_EINVAL, "vocab must be >= 2, got %d", vocab);
+  if (mask_index < 0 || mask_index >= vocab)
+    return fail(BD3_EINVAL, "mask_index %d outside [0, vocab = %d)", mask_index, vocab);
+  if (ld < vocab) return fail(BD3_EINVAL, "row stride ld (%lld) < vocab (%d)", (long long)ld, vocab);
+  if (logits_fp32 != 0 && logits_fp32 != 1) return fail(BD3_EINVAL, "logits_fp32 must be 0 (bf16) or 1 (fp32)");
+  if (!(keep >= 0.0 && keep <= 1.0)) return fail(BD3_EINVAL, "keep (s / t) must lie in [0, 1]");
+  if (rows > 0 && (logits == nullptr || xt == nullptr || out == nullptr))
+    return fail(BD3_EINVAL, "logits, xt and out must be non-NULL");
+  bd3::SubsArgs a;
+  a.logits = logits;
+  a.ld = ld;
+  a.fp32 = logits_fp32;
+  a.xt = xt;
+  a.out = out;
+  a.rows = rows;
+  a.vocab = vocab;
+  a.mask_index = mask_index;
+  a.keep = keep;
+  a.u = u;
+  a.seed = seed;
+  a.offset = offset;
+  return hip_status(bd3::launch_subs_sample(a, static_cast<hipStream_t>(stream)), "subs_sample launch");
+}
+
 int bd3_mask_dump(uint8_t* out, int32_t mode, int32_t rows, int32_t kv_len, int32_t block_size,
                   void* stream) {
   if (out == nullptr) return fail(BD3_EINVAL, "out is NULL");

@@ -227,6 +227,34 @@ int bd3_kv_write(const void* k, const void* v, void* k_dst, void* v_dst, int32_t
                  void* stream);
 
 /*
+ * One ancestral denoising step of BD3-LM sampling for `rows` token
+ * positions: SUBS parameterization of the logits (zero mass on [MASK],
+ * log-softmax), the categorical draw by Gumbel-max with float64 noise, and
+ * the carry-over of unmasked tokens, fused; no (rows, vocab) intermediate is
+ * written. Replaces subs_parameterization (model/subs.py:11-43) plus the
+ * sampler's update and sample_categorical (sample/sampler.py:110-122,
+ * :11-34):
+ *   out[r] = xt[r]                                   if xt[r] != mask_index
+ *          = argmax_i q_i / (1e-10 - log(u_i + 1e-10)) otherwise,
+ *   q_i = exp(log_softmax(logits + bias))_i * (1 - keep), q_mask = keep,
+ * keep = s / t of the step, with the reference's dtypes (bf16 logits: the
+ * bias add and the shift by the max in bf16, exp / sum / log in fp32; q,
+ * noise and ratio in float64).
+ *   logits: (rows, ld) device array, bf16 (logits_fp32 = 0) or fp32 (1);
+ *   xt, out: device int64 (rows); out may alias xt;
+ *   u: device float64 (rows, vocab) uniforms in [0, 1) (the reference's
+ *      torch.rand_like draw), or NULL to draw them with Philox4x32-10:
+ *      element e = r * vocab + i takes the 64 bits of words (0, 1) (e even)
+ *      or (2, 3) (e odd) of the block with counter
+ *      {e/2 low, e/2 high, offset low, offset high} and key {seed low,
+ *      seed high}, as (bits >> 11) * 2^-53.
+ * Logits must be finite. vocab in [2, 2^31), mask_index in [0, vocab).
+ */
+int bd3_subs_sample(const void* logits, int64_t ld, int32_t logits_fp32, const int64_t* xt,
+                    int64_t* out, int32_t rows, int32_t vocab, int32_t mask_index, double keep,
+                    const double* u, uint64_t seed, uint64_t offset, void* stream);
+
+/*
  * Writes the mask the device predicate applies, one byte per (row, key)
  * (1 = may attend), row-major:
  *   mode 0 (training): (2n, 2n) with n = rows, kv_len ignored;

@@ -182,3 +182,21 @@ def test_kv_write_validation(lib):
     expect_einval(lib.bd3_kv_write(GOOD, GOOD, None, GOOD, 1, 12, 32, 64, st, None), "k_dst is NULL")
     expect_einval(lib.bd3_kv_write(GOOD, GOOD, GOOD, GOOD, 1, 12, -2, 64, st, None), "seq >= 0")
     expect_einval(lib.bd3_kv_write(GOOD, GOOD, GOOD, GOOD, 1, 12, 32, 64, None, None), "strides is NULL")
+
+
+def test_subs_sample_validation(lib):
+    ok = dict(logits=GOOD, ld=1000, fp32=0, xt=GOOD, out=GOOD, rows=4, vocab=1000, mask=999, keep=0.5)
+
+    def call(**kw):
+        a = {**ok, **kw}
+        return lib.bd3_subs_sample(a["logits"], a["ld"], a["fp32"], a["xt"], a["out"], a["rows"], a["vocab"],
+                                   a["mask"], a["keep"], None, 0, 0, None)
+    expect_einval(call(vocab=1), "vocab must be >= 2")
+    expect_einval(call(mask=1000), "mask_index 1000 outside")
+    expect_einval(call(mask=-1), "mask_index -1 outside")
+    expect_einval(call(ld=999), "row stride ld")
+    expect_einval(call(fp32=2), "logits_fp32")
+    expect_einval(call(keep=1.5), "keep (s / t)")
+    expect_einval(call(keep=float("nan")), "keep (s / t)")
+    expect_einval(call(xt=None), "non-NULL")
+    expect_einval(call(rows=-1), "rows must be >= 0")
