@@ -27,6 +27,9 @@ Printed on stdout as ONE JSON line, with:
                 placement, bd3_qkv_rope) at configs[3]'s decode step and a
                 full 8 x 2048-token sequence, against the reference's eager
                 path (RoPE as bf16 ops + torch.cat of the cache);
+  sampling      one denoising step's SUBS + Gumbel-max draw
+                (bd3_subs_sample) at configs[4]'s and configs[3]'s step
+                shapes against the reference's eager float64 path;
   sweep         configs[2]: block sizes {4, 16, 64, 256} at B=4, L=2048,
                 H=16 (useful TFLOP/s and the schedule's useful fraction).
 Human-readable progress goes to stderr.
@@ -362,6 +365,57 @@ def kvcache_bench(device, reps: int):
     return out
 
 
+def sampling_bench(device, reps: int):
+    """One ancestral denoising step's SUBS + draw (bd3_subs_sample) against
+    the reference's eager path on the same GPU (model/subs.py:11-43 with the
+    reference's log_softmax, then sample/sampler.py:110-122 and :11-34 in
+    float64), at configs[4]'s step (8 sequences x 32-token blocks) and
+    configs[3]'s (32 x 16), vocab 50258, bf16 logits, 3/4 of the tokens
+    masked. `fused_philox_us`: noise drawn in-kernel; `fused_u_us`: the
+    caller's float64 uniforms read instead; `reference_eager_us` includes its
+    torch.rand_like draw. HIP events, 1 GiB cache flush before each rep."""
+    import torch
+    from kernels.sampling import PhiloxStream, subs_sample_step
+    from perf.harness import bench
+    V, mask = 50258, 50257
+    out = {}
+    for name, (B, L) in (("config4_step", (8, 32)), ("config3_step", (32, 16))):
+        g = torch.Generator(device=device).manual_seed(0)
+        logits = (torch.randn(B, L, V, device=device, generator=g) * 4).to(torch.bfloat16)
+        block = torch.randint(0, V - 1, (B, L), device=device, generator=g)
+        block[torch.rand(B, L, device=device, generator=g) < 0.75] = mask
+        u = torch.rand(B, L, V, device=device, dtype=torch.float64, generator=g)
+        keep = 0.5
+        gen = PhiloxStream(seed=1)
+
+        def eager():
+            bias = torch.zeros(V, device=device, dtype=logits.dtype)
+            bias[mask] = -1e6
+            x = logits + bias
+            sh = x - x.amax(dim=-1, keepdim=True)
+            lp = sh.float() - torch.log(torch.exp(sh.float()).sum(dim=-1, keepdim=True))
+            carry = torch.full_like(lp, -1e6).scatter(-1, block.unsqueeze(-1), 0.0)
+            lp = torch.where((block != mask).unsqueeze(-1), carry, lp)
+            q = torch.exp(lp).double() * (1 - keep)
+            q[..., mask] = keep
+            uu = torch.rand_like(q)
+            new = torch.argmax(q / (1e-10 - torch.log(uu + 1e-10)), dim=-1)
+            return torch.where(block != mask, block, new)
+
+        t_p = bench(lambda: subs_sample_step(logits, block, mask, keep, generator=gen), warmup=3, rep=reps,
+                    flush=True)
+        t_u = bench(lambda: subs_sample_step(logits, block, mask, keep, u=u), warmup=3, rep=reps, flush=True)
+        t_e = bench(eager, warmup=3, rep=reps, flush=True)
+        nbytes = logits.numel() * 2
+        out[name] = {"rows": B * L, "vocab": V, "fused_philox_us": t_p.median_ms * 1e3,
+                     "fused_u_us": t_u.median_ms * 1e3, "reference_eager_us": t_e.median_ms * 1e3,
+                     "logits_bytes": nbytes,
+                     "fused_philox_GB_s": nbytes / (t_p.median_ms * 1e-3) / 1e9}
+        del logits, block, u
+        torch.cuda.empty_cache()
+    return out
+
+
 def sweep_bench(device, steps: int, use_graph: bool = True):
     """B=4, L=2048, H=16, block sizes {4, 16, 64, 256}."""
     import torch
@@ -391,6 +445,7 @@ def main(argv=None) -> int:
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-kvcache", action="store_true")
+    ap.add_argument("--no-sampling", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a captured HIP graph")
     args = ap.parse_args(argv)
 
@@ -463,6 +518,11 @@ def main(argv=None) -> int:
             if k_ != "roofline":
                 log(f"kv_cache {k_}: kernel {r['kernel_us']:.1f} us ({r['kernel_GB_s']:.0f} GB/s), "
                     f"call {r['call_us']:.1f} us, reference eager {r['reference_eager_us']:.1f} us")
+    if not args.no_sampling:
+        result["sampling"] = sampling_bench(device, reps=20)
+        for k_, r in result["sampling"].items():
+            log(f"sampling {k_}: fused {r['fused_philox_us']:.1f} us (philox) / {r['fused_u_us']:.1f} us (given u), "
+                f"reference eager {r['reference_eager_us']:.1f} us")
     if not args.no_sweep:
         result["sweep"] = sweep_bench(device, steps=10, use_graph=not args.eager)
         for r in result["sweep"]:

@@ -20,9 +20,11 @@
 // seed with the 64-bit element-pair index and a 64-bit offset as counter, so
 // no noise tensor is materialised.
 //
-// One workgroup per row (256 threads): pass 1 the max, pass 2 the sum of
+// One workgroup per row (1024 threads; a row is long and rows are few, so
+// the parallelism is inside the row): pass 1 the max, pass 2 the sum of
 // exponentials, pass 3 the noisy ratio and its argmax (first index on ties,
-// as torch.argmax). The row is re-read from L2 / MALL in passes 2 and 3.
+// as torch.argmax). bf16 rows up to 65528 elements are staged in LDS with
+// 16-byte loads (one HBM read); others are re-read from L2 / MALL.
 // Logits must be finite (the token drawn for a row with NaN / inf logits is
 // unspecified).
 #include "bd3_device.h"
@@ -31,7 +33,7 @@
 namespace bd3 {
 namespace {
 
-constexpr int kSubsThreads = 256;
+constexpr int kSubsThreads = 1024;
 constexpr float kNegInf = -1e6f;   // model/subs.py:8
 constexpr double kEps = 1e-10;     // sample/sampler.py:8
 
@@ -73,10 +75,9 @@ __device__ __forceinline__ float load_logit<float>(const float* p, int i) {
   return p[i];
 }
 
-// x_i: the logit plus the [MASK] bias, rounded to the logits dtype.
+// x_i: the logit l of element i plus the [MASK] bias, rounded to the logits dtype.
 template <typename T>
-__device__ __forceinline__ float biased(const T* p, int i, int mask_index) {
-  const float l = load_logit<T>(p, i);
+__device__ __forceinline__ float biased(float l, int i, int mask_index) {
   if (i != mask_index) return l;
   if constexpr (sizeof(T) == 2) {
     return bf16_round(l + bf16_round(kNegInf));
@@ -127,11 +128,18 @@ __device__ __forceinline__ bool better(double v, int i, double bv, int bi) {
   return v > bv || (v == bv && i < bi);
 }
 
-template <typename T>
+// bf16 rows of up to kMaxStaged elements are copied to LDS once (16-byte
+// loads) and the three passes read them there; fp32 rows and longer bf16
+// rows are read from global memory in every pass.
+constexpr int kMaxStaged = 65536 - 8;
+
+template <typename T, bool STAGED>
 __global__ __launch_bounds__(kSubsThreads) void subs_sample_kernel(SubsArgs a) {
   __shared__ float red[kSubsThreads / 64];
   __shared__ double bval[kSubsThreads / 64];
   __shared__ int bidx[kSubsThreads / 64];
+  __shared__ __attribute__((aligned(16))) uint16_t srow[STAGED ? kMaxStaged + 8 : 8];
+  constexpr int NT = kSubsThreads;
   const int row = blockIdx.x;
   const int64_t xt = a.xt[row];
   if (xt != a.mask_index) {  // carry-over: an unmasked token stays (uniform per workgroup)
@@ -141,12 +149,47 @@ __global__ __launch_bounds__(kSubsThreads) void subs_sample_kernel(SubsArgs a) {
   const T* lp = static_cast<const T*>(a.logits) + (int64_t)row * a.ld;
   const int V = a.vocab;
 
+  // Element i sits at LDS slot i + sh, with sh chosen so that the first
+  // element on a 16-byte boundary of the row lands on a 16-byte slot.
+  int sh = 0;
+  if constexpr (STAGED) {
+    const uint16_t* p = reinterpret_cast<const uint16_t*>(lp);
+    const int mis = (int)(reinterpret_cast<uintptr_t>(p) & 15);  // even: bf16 rows are 2-byte aligned
+    int head = ((16 - mis) & 15) >> 1;                            // elements before that boundary
+    head = head < V ? head : V;
+    sh = (8 - head) & 7;
+    const int nb = (V - head) >> 3;
+    const int tail0 = head + 8 * nb;
+    if ((int)threadIdx.x < head) srow[threadIdx.x + sh] = p[threadIdx.x];
+    for (int k = threadIdx.x; k < nb; k += NT)
+      *reinterpret_cast<u32x4*>(&srow[head + sh + 8 * k]) = ld16(p + head + 8 * k);
+    if ((int)threadIdx.x < V - tail0) srow[tail0 + threadIdx.x + sh] = p[tail0 + threadIdx.x];
+    __syncthreads();
+  }
+  auto val = [&](int i) -> float {
+    if constexpr (STAGED) {
+      return __builtin_bit_cast(float, (uint32_t)srow[i + sh] << 16);
+    } else {
+      return load_logit<T>(lp, i);
+    }
+  };
   float m = -INFINITY;
-  for (int i = threadIdx.x; i < V; i += kSubsThreads) m = fmaxf(m, biased<T>(lp, i, a.mask_index));
+  for (int i = threadIdx.x; i < V; i += 4 * NT) {
+    float x[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) x[k] = i + k * NT < V ? biased<T>(val(i + k * NT), i + k * NT, a.mask_index) : -INFINITY;
+    m = fmaxf(m, fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
+  }
   m = block_max(m, red);
 
   float sum = 0.f;
-  for (int i = threadIdx.x; i < V; i += kSubsThreads) sum += expf(shifted<T>(biased<T>(lp, i, a.mask_index), m));
+  for (int i = threadIdx.x; i < V; i += 4 * NT) {
+    float x[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) x[k] = i + k * NT < V ? biased<T>(val(i + k * NT), i + k * NT, a.mask_index) : 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) sum += i + k * NT < V ? expf(shifted<T>(x[k], m)) : 0.f;
+  }
   const float lse = logf(block_sum(sum, red));
 
   const double keep = a.keep;         // s / t
@@ -154,47 +197,61 @@ __global__ __launch_bounds__(kSubsThreads) void subs_sample_kernel(SubsArgs a) {
   double best = -INFINITY;
   int besti = 0x7fffffff;
   const int64_t base = (int64_t)row * V;
-  for (int i0 = 2 * threadIdx.x; i0 < V; i0 += 2 * kSubsThreads) {
-    // two consecutive elements per Philox block pair (i0, i0 + 1)
-    double u[2];
+  // uniforms of elements i0 and i0 + 1 (i0 + 1 < V or ignored)
+  auto uniforms = [&](int i0, double& u0, double& u1) {
     if (a.u != nullptr) {
-      u[0] = a.u[base + i0];
-      u[1] = i0 + 1 < V ? a.u[base + i0 + 1] : 0.0;
+      u0 = a.u[base + i0];
+      u1 = i0 + 1 < V ? a.u[base + i0 + 1] : 0.0;
+      return;
+    }
+    const uint64_t e = (uint64_t)(base + i0);
+    const uint64_t pair = e >> 1;
+    uint32_t c[4] = {(uint32_t)pair, (uint32_t)(pair >> 32), (uint32_t)a.offset, (uint32_t)(a.offset >> 32)};
+    philox4x32_10(c, (uint32_t)a.seed, (uint32_t)(a.seed >> 32));
+    if ((e & 1) == 0) {  // element e uses words (0, 1), e + 1 words (2, 3)
+      u0 = u53(c[0], c[1]);
+      u1 = u53(c[2], c[3]);
+    } else {  // V odd, odd row: e + 1 starts the next pair
+      u0 = u53(c[2], c[3]);
+      const uint64_t p2 = pair + 1;
+      uint32_t d[4] = {(uint32_t)p2, (uint32_t)(p2 >> 32), (uint32_t)a.offset, (uint32_t)(a.offset >> 32)};
+      philox4x32_10(d, (uint32_t)a.seed, (uint32_t)(a.seed >> 32));
+      u1 = u53(d[0], d[1]);
+    }
+  };
+  // Pruning: -log(x) >= 1 - x, so the noise term g = EPS - log(u + EPS) is at
+  // least 1 - u and q / g <= q / (1 - u). An element with q / (1 - u) clearly
+  // below the running best cannot win, so its float64 log and division are
+  // skipped. The margin (1e-6 relative) covers the rounding of the computed
+  // g, whose relative error stays below 1e-10 while 1 - u > 1e-6 (u + EPS is
+  // rounded to 1.1e-16 absolute); elements with 1 - u <= 1e-6 always take the
+  // full path. The chosen token is unchanged.
+  auto consider = [&](int i, double u) {
+    double q;
+    if (i == a.mask_index) {
+      q = keep;
     } else {
-      const uint64_t pair = (uint64_t)(base + i0) >> 1;  // V may be odd: pair index of element base + i0
-      uint32_t c[4] = {(uint32_t)pair, (uint32_t)(pair >> 32), (uint32_t)a.offset,
-                       (uint32_t)(a.offset >> 32)};
-      philox4x32_10(c, (uint32_t)a.seed, (uint32_t)(a.seed >> 32));
-      // element e uses words (0, 1) if e is even, (2, 3) if odd
-      const bool odd = ((base + i0) & 1) != 0;
-      u[0] = odd ? u53(c[2], c[3]) : u53(c[0], c[1]);
-      if (!odd) {
-        u[1] = u53(c[2], c[3]);
-      } else {  // element base + i0 + 1 starts the next pair
-        const uint64_t p2 = pair + 1;
-        uint32_t d[4] = {(uint32_t)p2, (uint32_t)(p2 >> 32), (uint32_t)a.offset, (uint32_t)(a.offset >> 32)};
-        philox4x32_10(d, (uint32_t)a.seed, (uint32_t)(a.seed >> 32));
-        u[1] = u53(d[0], d[1]);
-      }
+      const float l = shifted<T>(biased<T>(val(i), i, a.mask_index), m) - lse;
+      q = (double)expf(l) * move;
     }
+    const double om = 1.0 - u;
+    if (om > 1e-6 && q < best * om * (1.0 - 1e-6)) return;
+    const double r = q / (kEps - log(u + kEps));
+    if (better(r, i, best, besti)) {
+      best = r;
+      besti = i;
+    }
+  };
+  // two independent element pairs per iteration
+  for (int i0 = 2 * threadIdx.x; i0 < V; i0 += 4 * NT) {
+    const int j0 = i0 + 2 * NT;
+    double u[4];
+    uniforms(i0, u[0], u[1]);
+    if (j0 < V) uniforms(j0, u[2], u[3]);
+    const int idx[4] = {i0, i0 + 1, j0, j0 + 1};
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int i = i0 + h;
-      if (i >= V) break;
-      double q;
-      if (i == a.mask_index) {
-        q = keep;
-      } else {
-        const float l = shifted<T>(biased<T>(lp, i, a.mask_index), m) - lse;
-        q = (double)expf(l) * move;
-      }
-      const double g = kEps - log(u[h] + kEps);
-      const double r = q / g;
-      if (better(r, i, best, besti)) {
-        best = r;
-        besti = i;
-      }
-    }
+    for (int h = 0; h < 4; ++h)
+      if (idx[h] < V) consider(idx[h], u[h]);
   }
   // argmax across the workgroup
 #pragma unroll
@@ -229,9 +286,11 @@ __global__ __launch_bounds__(kSubsThreads) void subs_sample_kernel(SubsArgs a) {
 hipError_t launch_subs_sample(const SubsArgs& a, hipStream_t stream) {
   if (a.rows == 0) return hipSuccess;
   if (a.fp32)
-    hipLaunchKernelGGL(subs_sample_kernel<float>, dim3(a.rows), dim3(kSubsThreads), 0, stream, a);
+    hipLaunchKernelGGL((subs_sample_kernel<float, false>), dim3(a.rows), dim3(kSubsThreads), 0, stream, a);
+  else if (a.vocab <= kMaxStaged)
+    hipLaunchKernelGGL((subs_sample_kernel<uint16_t, true>), dim3(a.rows), dim3(kSubsThreads), 0, stream, a);
   else
-    hipLaunchKernelGGL(subs_sample_kernel<uint16_t>, dim3(a.rows), dim3(kSubsThreads), 0, stream, a);
+    hipLaunchKernelGGL((subs_sample_kernel<uint16_t, false>), dim3(a.rows), dim3(kSubsThreads), 0, stream, a);
   return hipGetLastError();
 }
 
