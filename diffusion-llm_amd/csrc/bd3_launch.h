@@ -109,6 +109,19 @@ struct SubsArgs {
   uint64_t seed, offset;
 };
 
+struct GlueArgs {
+  const void* x;       // (batch, seq, d) rows, fp32 or bf16
+  const void* weight;  // (d) LayerNorm gain
+  const void* shift;   // (batch, d): shift (ln_modulate) or gate (gate_residual)
+  const void* scale;   // (batch, d)
+  const void* y;       // (batch, seq, d) sublayer output (gate_residual)
+  void* out;
+  int x_fp32, w_fp32, m_fp32, y_fp32, out_fp32;
+  int rows, seq, d;
+  int64_t sx_b, sx_s, sm_b, sy_b, sy_s, so_b, so_s;  // element strides
+  float eps;
+};
+
 hipError_t launch_attn_fwd(const FwdArgs& a, hipStream_t stream);
 hipError_t launch_attn_bwd_dq(const BwdArgs& a, hipStream_t stream);
 hipError_t launch_attn_bwd_dkdv(const BwdArgs& a, hipStream_t stream);
@@ -116,6 +129,8 @@ hipError_t launch_decode(const DecodeArgs& a, int qt, hipStream_t stream);
 hipError_t launch_qkv_rope(const QkvRopeArgs& a, hipStream_t stream);
 hipError_t launch_kv_write(const KvWriteArgs& a, hipStream_t stream);
 hipError_t launch_subs_sample(const SubsArgs& a, hipStream_t stream);
+hipError_t launch_ln_modulate(const GlueArgs& a, hipStream_t stream);
+hipError_t launch_gate_residual(const GlueArgs& a, hipStream_t stream);
 hipError_t launch_mask_dump(uint8_t* out, int mode, int rows, int kv_len,
                             int bs, hipStream_t stream);
 

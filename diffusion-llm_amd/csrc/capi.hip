@@ -419,6 +419,69 @@ int bd3_subs_sample(const void* logits, int64_t ld, int32_t logits_fp32, const i
   return hip_status(bd3::launch_subs_sample(a, static_cast<hipStream_t>(stream)), "subs_sample launch");
 }
 
+namespace {
+int check_glue_common(int batch, int seq, int d_model, const int64_t* strides, int n_strides,
+                      const int32_t* flags, int n_flags) {
+  if (batch < 1 || seq < 0) return fail(BD3_EINVAL, "need batch >= 1 and seq >= 0");
+  if (d_model < 8 || d_model % 8 != 0) return fail(BD3_EINVAL, "d_model must be a positive multiple of 8, got %d", d_model);
+  if ((int64_t)batch * seq >= ((int64_t)1 << 31)) return fail(BD3_EINVAL, "batch * seq too large");
+  if (strides == nullptr) return fail(BD3_EINVAL, "strides is NULL");
+  for (int i = 0; i < n_strides; ++i)
+    if (strides[i] < 0 || strides[i] % 8 != 0)
+      return fail(BD3_EINVAL, "stride[%d]=%lld must be a non-negative multiple of 8", i, (long long)strides[i]);
+  for (int i = 0; i < n_flags; ++i)
+    if (flags[i] != 0 && flags[i] != 1) return fail(BD3_EINVAL, "dtype flags must be 0 (bf16) or 1 (fp32)");
+  return BD3_OK;
+}
+int check_ptrs(const void* const* p, const char* const* names, int n) {
+  for (int i = 0; i < n; ++i) {
+    if (p[i] == nullptr) return fail(BD3_EINVAL, "%s is NULL", names[i]);
+    if (!aligned16(p[i])) return fail(BD3_EINVAL, "%s must be 16-byte aligned", names[i]);
+  }
+  return BD3_OK;
+}
+}  // namespace
+
+int bd3_ln_modulate(const void* x, int32_t x_fp32, const void* weight, int32_t weight_fp32,
+                    const void* shift, const void* scale, int32_t mod_fp32, void* out,
+                    int32_t out_fp32, int32_t batch, int32_t seq, int32_t d_model,
+                    const int64_t* strides, float eps, void* stream) {
+  const int32_t flags[4] = {x_fp32, weight_fp32, mod_fp32, out_fp32};
+  int st = check_glue_common(batch, seq, d_model, strides, 5, flags, 4);
+  if (st) return st;
+  const void* ptrs[5] = {x, weight, shift, scale, out};
+  const char* names[5] = {"x", "weight", "shift", "scale", "out"};
+  if ((st = check_ptrs(ptrs, names, 5))) return st;
+  if (!x_fp32 && !mod_fp32 && out_fp32)
+    return fail(BD3_EINVAL, "bf16 x with bf16 shift / scale modulates in bf16: out must be bf16");
+  if (!(eps >= 0.f)) return fail(BD3_EINVAL, "eps must be >= 0");
+  bd3::GlueArgs a = {};
+  a.x = x; a.weight = weight; a.shift = shift; a.scale = scale; a.out = out;
+  a.x_fp32 = x_fp32; a.w_fp32 = weight_fp32; a.m_fp32 = mod_fp32; a.out_fp32 = out_fp32;
+  a.rows = batch * seq; a.seq = seq > 0 ? seq : 1; a.d = d_model;
+  a.sx_b = strides[0]; a.sx_s = strides[1]; a.sm_b = strides[2]; a.so_b = strides[3]; a.so_s = strides[4];
+  a.eps = eps;
+  return hip_status(bd3::launch_ln_modulate(a, static_cast<hipStream_t>(stream)), "ln_modulate launch");
+}
+
+int bd3_gate_residual(const void* x, int32_t x_fp32, const void* gate, int32_t gate_fp32,
+                      const void* y, int32_t y_fp32, void* out, int32_t batch, int32_t seq,
+                      int32_t d_model, const int64_t* strides, void* stream) {
+  const int32_t flags[3] = {x_fp32, gate_fp32, y_fp32};
+  int st = check_glue_common(batch, seq, d_model, strides, 7, flags, 3);
+  if (st) return st;
+  const void* ptrs[4] = {x, gate, y, out};
+  const char* names[4] = {"x", "gate", "y", "out"};
+  if ((st = check_ptrs(ptrs, names, 4))) return st;
+  bd3::GlueArgs a = {};
+  a.x = x; a.shift = gate; a.y = y; a.out = out;
+  a.x_fp32 = x_fp32; a.m_fp32 = gate_fp32; a.y_fp32 = y_fp32;
+  a.rows = batch * seq; a.seq = seq > 0 ? seq : 1; a.d = d_model;
+  a.sx_b = strides[0]; a.sx_s = strides[1]; a.sm_b = strides[2]; a.sy_b = strides[3]; a.sy_s = strides[4];
+  a.so_b = strides[5]; a.so_s = strides[6];
+  return hip_status(bd3::launch_gate_residual(a, static_cast<hipStream_t>(stream)), "gate_residual launch");
+}
+
 int bd3_mask_dump(uint8_t* out, int32_t mode, int32_t rows, int32_t kv_len, int32_t block_size,
                   void* stream) {
   if (out == nullptr) return fail(BD3_EINVAL, "out is NULL");

@@ -255,6 +255,43 @@ int bd3_subs_sample(const void* logits, int64_t ld, int32_t logits_fp32, const i
                     const double* u, uint64_t seed, uint64_t offset, void* stream);
 
 /*
+ * modulate(LN(x), shift, scale) of a DiT block's pre-norm (weight-only
+ * LayerNorm, model/modules.py:243-288; modulate, :778-788; call sites in
+ * DiTBlock.forward, :537-568), one pass over x:
+ *   y = (weight * (x - mean)) * rsqrt(var + eps)   fp32 over the upcast row,
+ *       var with correction 0, then cast back to x's dtype;
+ *   out = y * (1 + scale) + shift                  1 + scale in the vectors'
+ *       dtype; the product and sum in bf16 op by op if x and the vectors
+ *       are bf16, else in fp32;
+ * out is written in that dtype, or rounded to bf16 (out_fp32 = 0) when it is
+ * fp32 (the cast autocast applies at the next matmul's input).
+ *   x, out: (batch, seq, d_model); shift, scale: (batch, d_model) (the
+ *   reference's (batch, 1, d_model) broadcast); weight: (d_model).
+ *   *_fp32: 1 = fp32, 0 = bf16 for each operand.
+ *   strides: 5 element strides: x (batch, seq), shift / scale (batch), out
+ *   (batch, seq); last strides 1; bases 16-byte aligned, strides and d_model
+ *   multiples of 8.
+ */
+int bd3_ln_modulate(const void* x, int32_t x_fp32, const void* weight, int32_t weight_fp32,
+                    const void* shift, const void* scale, int32_t mod_fp32, void* out,
+                    int32_t out_fp32, int32_t batch, int32_t seq, int32_t d_model,
+                    const int64_t* strides, float eps, void* stream);
+
+/*
+ * out = x + gate * y, the residual updates of DiTBlock.forward
+ * (model/modules.py:560-566): gate * y in bf16 if both are bf16 (rounded)
+ * else fp32, then the add in bf16 if x and that product are bf16 else fp32;
+ * out has that dtype (bf16 only when x, gate and y all are). Bit-exact with
+ * the eager ops; out may alias x.
+ *   x, y, out: (batch, seq, d_model); gate: (batch, d_model).
+ *   strides: 7 element strides: x (batch, seq), gate (batch), y (batch,
+ *   seq), out (batch, seq); same alignment rules as bd3_ln_modulate.
+ */
+int bd3_gate_residual(const void* x, int32_t x_fp32, const void* gate, int32_t gate_fp32,
+                      const void* y, int32_t y_fp32, void* out, int32_t batch, int32_t seq,
+                      int32_t d_model, const int64_t* strides, void* stream);
+
+/*
  * Writes the mask the device predicate applies, one byte per (row, key)
  * (1 = may attend), row-major:
  *   mode 0 (training): (2n, 2n) with n = rows, kv_len ignored;

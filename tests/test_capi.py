@@ -200,3 +200,22 @@ def test_subs_sample_validation(lib):
     expect_einval(call(keep=float("nan")), "keep (s / t)")
     expect_einval(call(xt=None), "non-NULL")
     expect_einval(call(rows=-1), "rows must be >= 0")
+
+
+def test_dit_glue_validation(lib):
+    st5 = _i64([768 * 16, 768, 768, 768 * 16, 768])
+    st7 = _i64([768 * 16, 768, 768, 768 * 16, 768, 768 * 16, 768])
+    ln = lambda **kw: lib.bd3_ln_modulate(kw.get("x", GOOD), kw.get("xf", 1), GOOD, 1, GOOD, GOOD, kw.get("mf", 0),
+                                          GOOD, kw.get("of", 1), 2, 16, kw.get("d", 768), kw.get("st", st5),
+                                          kw.get("eps", 1e-5), None)
+    expect_einval(ln(d=100), "multiple of 8")
+    expect_einval(ln(x=GOOD + 8), "x must be 16-byte aligned")
+    expect_einval(ln(xf=2), "dtype flags")
+    expect_einval(ln(xf=0, mf=0, of=1), "out must be bf16")
+    expect_einval(ln(st=_i64([768 * 16, 770, 768, 768 * 16, 768])), "stride[1]")
+    expect_einval(ln(eps=-1.0), "eps")
+    gr = lambda **kw: lib.bd3_gate_residual(GOOD, 1, kw.get("g", GOOD), 0, GOOD, 0, GOOD, 2, 16, kw.get("d", 768),
+                                            kw.get("st", st7), None)
+    expect_einval(gr(g=None), "gate is NULL")
+    expect_einval(gr(d=0), "multiple of 8")
+    expect_einval(gr(st=None), "strides is NULL")

@@ -1,0 +1,67 @@
+"""GPU parity of the fused DiT glue (bd3_ln_modulate, bd3_gate_residual)
+against oracle/dit.py: the gated residual bit-exact in every dtype mix;
+LayerNorm + modulate within the rounding its fp32 row statistics allow
+(summation order differs): fp32 results within 1e-5 relative, bf16 results
+within one bf16 ulp per rounding of the magnitudes entering the last add, at most 1% of
+elements off by any amount."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from kernels.dit_glue import gate_residual, ln_modulate
+from oracle.dit import gate_residual as ref_gate
+from oracle.dit import layer_norm as ref_layer_norm
+from oracle.dit import ln_modulate as ref_lnmod
+
+F32, BF = torch.float32, torch.bfloat16
+
+
+def rnd(shape, dtype, seed, scale=1.0, shift=0.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale + shift).to(dtype)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("xd,md,od", [(F32, BF, F32), (F32, BF, BF), (BF, BF, BF), (BF, F32, F32), (F32, F32, F32)])
+@pytest.mark.parametrize("B,S,D", [(2, 37, 768), (1, 5, 64), (8, 256, 768)])
+def test_ln_modulate(cuda, xd, md, od, B, S, D):
+    print(f"ln_modulate x={xd} mod={md} out={od} shape=({B},{S},{D})", flush=True)
+    x = rnd((B, S, D), xd, 1, scale=2.0, shift=0.3)
+    w = rnd((D,), F32, 2, scale=0.2, shift=1.0)
+    sh, sc = rnd((B, D), md, 3, 0.5), rnd((B, D), md, 4, 0.5)
+    want = ref_lnmod(x, w, sh, sc)
+    got = ln_modulate(x.to(cuda), w.to(cuda), sh.to(cuda)[:, None], sc.to(cuda)[:, None],
+                      out_dtype=od if od != want.dtype else None).cpu()
+    assert got.dtype == od
+    if od == F32 and xd == F32:
+        assert torch.allclose(got, want.float(), rtol=1e-5, atol=1e-5)
+    else:
+        # A row statistic one fp32 ulp off can move a rounding to bf16 (of y
+        # when x is bf16, then of the product and of the sum on the bf16
+        # path) by one bf16 ulp each, i.e. at most 2^-7 relative per rounding:
+        # within 3 * 2^-7 of the magnitudes entering the last add.
+        h = ref_layer_norm(x, w).float()
+        mag = (h * (1 + sc.float()[:, None])).abs() + sh.float()[:, None].abs()
+        diff = (got.float() - want.to(od).float()).abs()
+        assert (diff <= 3 * 2.0 ** -7 * mag + 1e-30).all(), float((diff / (mag + 1e-30)).max())
+        assert (diff > 0).float().mean() < 0.01, float((diff > 0).float().mean())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("xd,gd,yd", [(F32, BF, BF), (BF, BF, BF), (F32, F32, F32), (BF, F32, BF)])
+def test_gate_residual_bit_exact(cuda, xd, gd, yd):
+    B, S, D = 3, 50, 768
+    x, g, y = rnd((B, S, D), xd, 5), rnd((B, D), gd, 6), rnd((B, S, D), yd, 7)
+    want = ref_gate(x, g, y)
+    got = gate_residual(x.to(cuda), g.to(cuda)[:, None], y.to(cuda)).cpu()
+    assert got.dtype == want.dtype and torch.equal(got, want)
+
+
+@pytest.mark.gpu
+def test_gate_residual_in_place(cuda):
+    x = rnd((2, 16, 64), F32, 8).to(cuda)
+    g, y = rnd((2, 64), BF, 9).to(cuda), rnd((2, 16, 64), BF, 10).to(cuda)
+    want = ref_gate(x.cpu(), g.cpu(), y.cpu())
+    out = gate_residual(x, g, y, out=x)
+    assert out.data_ptr() == x.data_ptr() and torch.equal(x.cpu(), want)
