@@ -30,6 +30,9 @@ Printed on stdout as ONE JSON line, with:
   sampling      one denoising step's SUBS + Gumbel-max draw
                 (bd3_subs_sample) at configs[4]'s and configs[3]'s step
                 shapes against the reference's eager float64 path;
+  dit_glue      LayerNorm + adaLN modulate and the gated residual
+                (bd3_ln_modulate, bd3_gate_residual) at configs[1]'s and
+                configs[4]'s shapes against the reference's eager ops;
   sweep         configs[2]: block sizes {4, 16, 64, 256} at B=4, L=2048,
                 H=16 (useful TFLOP/s and the schedule's useful fraction).
 Human-readable progress goes to stderr.
@@ -416,6 +419,53 @@ def sampling_bench(device, reps: int):
     return out
 
 
+def glue_bench(device, reps: int):
+    """The DiT block's glue around attention at configs[1]'s training shape
+    (8 x 2048 tokens, d_model 768; fp32 residual, bf16 adaLN vectors, bf16
+    result for the next matmul) and configs[4]'s sampling step (8 x 32
+    tokens, all bf16): bd3_ln_modulate and bd3_gate_residual against the
+    reference's eager ops on the same GPU (model/modules.py:243-288,
+    :778-788, :560-566). HIP events, 1 GiB cache flush before each rep."""
+    import torch
+    from kernels.dit_glue import gate_residual, ln_modulate
+    from perf.harness import bench
+    out = {}
+    for name, (B, S, xd) in (("training", (8, 2048, torch.float32)), ("sampling_step", (8, 32, torch.bfloat16))):
+        D = 768
+        g = torch.Generator(device=device).manual_seed(0)
+        x = torch.randn(B, S, D, device=device, generator=g).to(xd)
+        w = torch.rand(D, device=device, generator=g) + 0.5
+        sh, sc, gt = (torch.randn(B, 1, D, device=device, generator=g).to(torch.bfloat16) for _ in range(3))
+        y = torch.randn(B, S, D, device=device, generator=g).to(torch.bfloat16)
+
+        def eager_ln():
+            xf = x.float()
+            num = xf - xf.mean(dim=-1, keepdim=True)
+            inv = torch.rsqrt(xf.var(dim=-1, keepdim=True, correction=0) + 1e-5)
+            h = (w * num * inv).to(x.dtype)
+            return (h * (1 + sc) + sh).to(torch.bfloat16)
+
+        t_ln = bench(lambda: ln_modulate(x, w, sh, sc, out_dtype=torch.bfloat16), warmup=3, rep=reps, flush=True)
+        t_ln_e = bench(eager_ln, warmup=3, rep=reps, flush=True)
+        t_gr = bench(lambda: gate_residual(x, gt, y), warmup=3, rep=reps, flush=True)
+        t_gr_e = bench(lambda: x + gt * y, warmup=3, rep=reps, flush=True)
+        xb = x.element_size()
+        ln_bytes = B * S * D * (xb + 2)            # x read, bf16 result written
+        gr_bytes = B * S * D * (2 * xb + 2)        # x and y read, result (x's dtype) written
+        out[name] = {"batch": B, "tokens": S, "d_model": D, "x_dtype": str(xd).replace("torch.", ""),
+                     "ln_modulate_us": t_ln.median_ms * 1e3, "ln_modulate_reference_eager_us": t_ln_e.median_ms * 1e3,
+                     "ln_modulate_GB_s": ln_bytes / (t_ln.median_ms * 1e-3) / 1e9,
+                     "gate_residual_us": t_gr.median_ms * 1e3, "gate_residual_reference_eager_us": t_gr_e.median_ms * 1e3,
+                     "gate_residual_GB_s": gr_bytes / (t_gr.median_ms * 1e-3) / 1e9}
+        del x, y
+        torch.cuda.empty_cache()
+    tr = out["training"]
+    out["roofline"] = {"bound": "hbm", "achieved": tr["ln_modulate_GB_s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                       "frac": tr["ln_modulate_GB_s"] / PEAK_HBM_GBS, "traffic": measured_traffic("ln_modulate_kernel"),
+                       "kernel": "ln_modulate_kernel (training)"}
+    return out
+
+
 def sweep_bench(device, steps: int, use_graph: bool = True):
     """B=4, L=2048, H=16, block sizes {4, 16, 64, 256}."""
     import torch
@@ -446,6 +496,7 @@ def main(argv=None) -> int:
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-kvcache", action="store_true")
     ap.add_argument("--no-sampling", action="store_true")
+    ap.add_argument("--no-glue", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a captured HIP graph")
     args = ap.parse_args(argv)
 
@@ -523,6 +574,13 @@ def main(argv=None) -> int:
         for k_, r in result["sampling"].items():
             log(f"sampling {k_}: fused {r['fused_philox_us']:.1f} us (philox) / {r['fused_u_us']:.1f} us (given u), "
                 f"reference eager {r['reference_eager_us']:.1f} us")
+    if not args.no_glue:
+        result["dit_glue"] = glue_bench(device, reps=20)
+        for k_, r in result["dit_glue"].items():
+            if k_ != "roofline":
+                log(f"dit_glue {k_}: ln_modulate {r['ln_modulate_us']:.1f} us ({r['ln_modulate_GB_s']:.0f} GB/s, "
+                    f"eager {r['ln_modulate_reference_eager_us']:.1f} us), gate_residual {r['gate_residual_us']:.1f} us "
+                    f"({r['gate_residual_GB_s']:.0f} GB/s, eager {r['gate_residual_reference_eager_us']:.1f} us)")
     if not args.no_sweep:
         result["sweep"] = sweep_bench(device, steps=10, use_graph=not args.eager)
         for r in result["sweep"]:

@@ -455,6 +455,7 @@ int bd3_ln_modulate(const void* x, int32_t x_fp32, const void* weight, int32_t w
   if (!x_fp32 && !mod_fp32 && out_fp32)
     return fail(BD3_EINVAL, "bf16 x with bf16 shift / scale modulates in bf16: out must be bf16");
   if (!(eps >= 0.f)) return fail(BD3_EINVAL, "eps must be >= 0");
+  if (d_model > 4096) return fail(BD3_EINVAL, "d_model must be <= 4096, got %d", d_model);
   bd3::GlueArgs a = {};
   a.x = x; a.weight = weight; a.shift = shift; a.scale = scale; a.out = out;
   a.x_fp32 = x_fp32; a.w_fp32 = weight_fp32; a.m_fp32 = mod_fp32; a.out_fp32 = out_fp32;

@@ -12,7 +12,7 @@
 //     rounded, as eager bf16 tensor ops; fp32 otherwise), optionally rounded
 //     to bf16 for the next matmul (what autocast does at its input).
 //   One wavefront per row (64 lanes x 16-byte chunks); the row is read from
-//   HBM once and re-read from L1 / L2 for the variance and the output.
+//   HBM once and kept in registers (d_model <= 4096).
 // gate_residual_kernel: x + gate * y (the residual updates of
 //   DiTBlock.forward, :560-566): gate * y in the promoted dtype of gate and y,
 //   then the add in the promoted dtype of x and that product; bit-exact with
@@ -64,6 +64,9 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// CH: 16-byte chunks (8 elements) of the row held per lane; the row is read
+// from HBM once into registers (d_model <= 512 * CH).
+template <int CH>
 __global__ __launch_bounds__(256) void ln_modulate_kernel(GlueArgs a) {
 #pragma clang fp contract(off)  // separate products and sums, as the eager ops
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -74,43 +77,52 @@ __global__ __launch_bounds__(256) void ln_modulate_kernel(GlueArgs a) {
   const int nch = D >> 3;
   const void* xr = elem(a.x, a.x_fp32, b * a.sx_b + s * a.sx_s);
 
+  float v[CH][8];
   float sum = 0.f;
-  for (int c = lane; c < nch; c += 64) {
-    float v[8];
-    load8(elem(xr, a.x_fp32, 8 * c), a.x_fp32, v);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) sum += v[k];
+  for (int k = 0; k < CH; ++k) {
+    const int c = lane + 64 * k;
+    if (c < nch) {
+      load8(elem(xr, a.x_fp32, 8 * c), a.x_fp32, v[k]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[k][e] = 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sum += v[k][e];
   }
   const float mean = wave_sum(sum) / (float)D;
   float sq = 0.f;
-  for (int c = lane; c < nch; c += 64) {
-    float v[8];
-    load8(elem(xr, a.x_fp32, 8 * c), a.x_fp32, v);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const float dlt = v[k] - mean;
-      sq += dlt * dlt;
+  for (int k = 0; k < CH; ++k)
+    if (lane + 64 * k < nch) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float dlt = v[k][e] - mean;
+        sq += dlt * dlt;
+      }
     }
-  }
   const float inv = rsqrtf(wave_sum(sq) / (float)D + a.eps);
 
   const bool mod_bf16 = !a.x_fp32 && !a.m_fp32;  // modulate in bf16 iff y and the vectors are bf16
   const void* shr = elem(a.shift, a.m_fp32, b * a.sm_b);
   const void* scr = elem(a.scale, a.m_fp32, b * a.sm_b);
   void* outr = const_cast<char*>(elem(a.out, a.out_fp32, b * a.so_b + s * a.so_s));
-  for (int c = lane; c < nch; c += 64) {
-    float v[8], w[8], sh[8], sc[8], o[8];
-    load8(elem(xr, a.x_fp32, 8 * c), a.x_fp32, v);
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    const int c = lane + 64 * k;
+    if (c >= nch) break;
+    float w[8], sh[8], sc[8], o[8];
     load8(elem(a.weight, a.w_fp32, 8 * c), a.w_fp32, w);
     load8(elem(shr, a.m_fp32, 8 * c), a.m_fp32, sh);
     load8(elem(scr, a.m_fp32, 8 * c), a.m_fp32, sc);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      float y = (w[k] * (v[k] - mean)) * inv;
+    for (int e = 0; e < 8; ++e) {
+      float y = (w[e] * (v[k][e] - mean)) * inv;
       if (!a.x_fp32) y = rbf(y);  // .to(original dtype)
       // 1 + scale keeps scale's dtype (a Python scalar does not promote)
-      const float t = a.m_fp32 ? 1.f + sc[k] : rbf(1.f + sc[k]);
-      o[k] = mod_bf16 ? rbf(rbf(y * t) + sh[k]) : y * t + sh[k];
+      const float t = a.m_fp32 ? 1.f + sc[e] : rbf(1.f + sc[e]);
+      o[e] = mod_bf16 ? rbf(rbf(y * t) + sh[e]) : y * t + sh[e];
     }
     store8(static_cast<char*>(outr) + (int64_t)8 * c * (a.out_fp32 ? 4 : 2), a.out_fp32, o);
   }
@@ -142,7 +154,18 @@ __global__ __launch_bounds__(256) void gate_residual_kernel(GlueArgs a) {
 
 hipError_t launch_ln_modulate(const GlueArgs& a, hipStream_t stream) {
   if (a.rows == 0) return hipSuccess;
-  hipLaunchKernelGGL(ln_modulate_kernel, dim3((unsigned)((a.rows + 3) / 4)), dim3(256), 0, stream, a);
+  const dim3 grid((unsigned)((a.rows + 3) / 4));
+  const int ch = (a.d / 8 + 63) / 64;  // chunks per lane
+  if (ch <= 1)
+    hipLaunchKernelGGL(ln_modulate_kernel<1>, grid, dim3(256), 0, stream, a);
+  else if (ch <= 2)
+    hipLaunchKernelGGL(ln_modulate_kernel<2>, grid, dim3(256), 0, stream, a);
+  else if (ch <= 4)
+    hipLaunchKernelGGL(ln_modulate_kernel<4>, grid, dim3(256), 0, stream, a);
+  else if (ch <= 8)
+    hipLaunchKernelGGL(ln_modulate_kernel<8>, grid, dim3(256), 0, stream, a);
+  else
+    return hipErrorInvalidValue;  // d_model > 4096: rejected by the C ABI
   return hipGetLastError();
 }
 

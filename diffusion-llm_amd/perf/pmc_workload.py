@@ -12,7 +12,9 @@ Dispatches, in order and each `--reps` times:
   3. the split-KV decode at configs[3] (32 x 12 heads, q_len 16,
      kv_len 4112) with the library's automatic split count;
   4. the layer's attention inputs (bd3_qkv_rope: head split + RoPE) over a
-     full 8 x 2048-token sequence, 12 heads.
+     full 8 x 2048-token sequence, 12 heads;
+  5. LayerNorm + adaLN modulate (bd3_ln_modulate) over 8 x 2048 tokens of
+     d_model 768 (fp32 residual, bf16 vectors, bf16 result).
 No timing is done here; the profiler records per-dispatch counters.
 """
 from __future__ import annotations
@@ -90,6 +92,16 @@ def main(argv=None) -> int:
                              ptr(vo), st, stream_of(qkv)))
     torch.cuda.synchronize()
     print(f"qkv_rope done (projection bytes read per dispatch {qkv.numel() * 2})", flush=True)
+    del qkv, qo, ko, vo
+
+    from kernels.dit_glue import ln_modulate
+    x = torch.randn(8, 2048, 768, device=dev)
+    w = torch.ones(768, device=dev)
+    sh = torch.zeros(8, 1, 768, device=dev, dtype=torch.bfloat16)
+    for _ in range(args.reps):
+        ln_modulate(x, w, sh, sh, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    print(f"ln_modulate done (x bytes read per dispatch {x.numel() * 4})", flush=True)
     return 0
 
 

@@ -270,7 +270,7 @@ int bd3_subs_sample(const void* logits, int64_t ld, int32_t logits_fp32, const i
  *   *_fp32: 1 = fp32, 0 = bf16 for each operand.
  *   strides: 5 element strides: x (batch, seq), shift / scale (batch), out
  *   (batch, seq); last strides 1; bases 16-byte aligned, strides and d_model
- *   multiples of 8.
+ *   multiples of 8; d_model <= 4096.
  */
 int bd3_ln_modulate(const void* x, int32_t x_fp32, const void* weight, int32_t weight_fp32,
                     const void* shift, const void* scale, int32_t mod_fp32, void* out,
