@@ -98,7 +98,7 @@ class TrainStep:
         self.o = torch.empty_like(self.q)
         self.lse = torch.empty((B, H, 2 * n), device=device, dtype=torch.float32)
         self.dq, self.dk, self.dv = (torch.empty_like(self.q) for _ in range(3))
-        self.delta = torch.empty((B, H, 2 * n), device=device, dtype=torch.float32)
+        self.delta = torch.empty((2, B, H, 2 * n), device=device, dtype=torch.float32)  # Delta, L * log2(e)
         self.lib = lib()
         self.fwd_strides = strides(self.q, self.k, self.v, self.o)
         self.dq_strides = strides(self.q, self.k, self.v, self.o, self.do, self.dq)

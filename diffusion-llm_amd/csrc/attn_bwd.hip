@@ -17,10 +17,11 @@
 //   L and Delta are per-lane scalars; dQ^T += K^T dS^T reads K^T from the LDS
 //   tile with ds_read_b64_tr_b16. Delta = rowsum(dO o O) is formed here from
 //   the row registers and stored for the second kernel (this fuses the
-//   reference's separate Delta op).
+//   reference's separate Delta op), next to the rows' L * log2(e), so the
+//   second kernel's exponent is one fma per element.
 // attn_bwd_dkdv_dma_kernel (key-stationary): 4 waves of 32 keys. K and V rows
 //   live in registers as B operands of S = Q K^T and dP = dO V^T, which put
-//   one key per lane; query tiles (Q, dO, L, Delta) come through LDS.
+//   one key per lane; query tiles (Q, dO, L * log2(e), Delta) come through LDS.
 //   dV += P^T dO and dK += dS^T Q take P^T / dS^T straight from registers and
 //   dO / Q transposed from LDS. dK, dV are written through LDS as 16-byte rows.
 // Both load their tiles global -> LDS with global_load_lds into three-stage
@@ -46,8 +47,8 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dkdv_dma_kernel(BwdArgs a) 
   constexpr int kBK = 128;  // keys per workgroup: 4 waves x 32
   constexpr int kStages = 3;
   // Stage layout (bytes): Q tile [0, 8K), dO tile [8K, 16K), row scalars
-  // [16K, 17K): L of the 64 rows, then Delta, then both again (the load that
-  // fetches them writes 1 KB).
+  // [16K, 17K): L * log2(e) of the 64 rows, then Delta, then both again (the
+  // load that fetches them writes 1 KB).
   constexpr int kStageBytes = 4 * kSwTile + 1024;
   __shared__ __attribute__((aligned(1024))) __bf16 smem[kStages * kStageBytes / 2];
 
@@ -94,7 +95,8 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dkdv_dma_kernel(BwdArgs a) 
     qoff[j] = (uint32_t)(2 * (r * (int)a.sq.s + ch));
     dooff[j] = (uint32_t)(2 * (r * (int)a.sdo.s + ch));
   }
-  const float* scal_src = ((lane & 16) ? a.delta : a.lse) + rowbase + 4 * (lane & 15);
+  // L comes as L * log2(e), the second plane of the delta buffer (written by the dQ kernel).
+  const float* scal_src = ((lane & 16) ? a.delta : a.delta + (int64_t)a.bh * 2 * a.n) + rowbase + 4 * (lane & 15);
   const int64_t qstep = (int64_t)kSwRows * a.sq.s, dostep = (int64_t)kSwRows * a.sdo.s;
   const uint32_t lds0 = lds_addr(&smem[0]);
   auto issue = [&](int i, int stage) {
@@ -166,7 +168,7 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dkdv_dma_kernel(BwdArgs a) 
     for (int rg = 0; rg < 4; ++rg) {
       const f32x4 lr = *reinterpret_cast<const f32x4*>(&scal[32 * qb + 8 * rg + 4 * g]);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) p[4 * rg + j] = fast_exp2(fmaf(s[4 * rg + j], a.scale_log2, -lr[j] * kLog2e));
+      for (int j = 0; j < 4; ++j) p[4 * rg + j] = fast_exp2(fmaf(s[4 * rg + j], a.scale_log2, -lr[j]));
     }
     if (masked) {
       if (MASK16) {
@@ -335,7 +337,10 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dq_dma_kernel(BwdArgs a) {
     for (int j = 0; j < 8; ++j) dsum = fmaf((float)doreg[c][j], (float)oreg[c][j], dsum);
   const float drow = sum_xor32(dsum);
   const float lrow = lse_row * kLog2e;
-  if (g == 0) a.delta[rowbase + myq] = drow;
+  if (g == 0) {
+    a.delta[rowbase + myq] = drow;
+    a.delta[(int64_t)a.bh * 2 * a.n + rowbase + myq] = lrow;  // second plane: L * log2(e) for dK/dV
+  }
 #pragma unroll
   for (int c = 0; c < 4; ++c) asm volatile("" ::"v"(qreg[c]), "v"(doreg[c]));
   const RowIntervals riv = train_row_intervals(myq, a.n, a.bs);

@@ -202,7 +202,7 @@ int bd3_attn_fwd(const void* q, const void* k, const void* v, void* o, float* ls
 
 size_t bd3_attn_bwd_workspace_bytes(int32_t batch, int32_t heads, int32_t n, int32_t head_dim) {
   if (batch < 1 || heads < 1 || n < 1 || head_dim < 1) return 0;
-  return align256((size_t)batch * heads * 2 * n * sizeof(float));  // Delta
+  return align256(2 * (size_t)batch * heads * 2 * n * sizeof(float));  // Delta, L * log2(e)
 }
 
 int bd3_attn_bwd_dq(const void* q, const void* k, const void* v, const void* o, const void* dout,

@@ -69,9 +69,10 @@ int bd3_attn_fwd(const void* q, const void* k, const void* v, void* o,
                  float scale, void* stream);
 
 /*
- * Bytes of workspace bd3_attn_bwd needs: Delta = rowsum(dO * O), fp32,
- * (batch, heads, 2n). No reference counterpart (the reference allocates
- * Delta with a torch op, kernels/BlockSparseFlashAttention.py:525).
+ * Bytes of workspace bd3_attn_bwd needs: two fp32 (batch, heads, 2n)
+ * planes, Delta = rowsum(dO * O) and L * log2(e). No reference counterpart
+ * (the reference allocates Delta with a torch op,
+ * kernels/BlockSparseFlashAttention.py:525).
  */
 size_t bd3_attn_bwd_workspace_bytes(int32_t batch, int32_t heads, int32_t n,
                                     int32_t head_dim);
@@ -79,7 +80,7 @@ size_t bd3_attn_bwd_workspace_bytes(int32_t batch, int32_t heads, int32_t n,
 /*
  * Training attention backward: dQ, dK, dV of the forward above, given
  * dO and the forward's O and lse. Runs bd3_attn_bwd_dq then
- * bd3_attn_bwd_dkdv with Delta in the workspace.
+ * bd3_attn_bwd_dkdv with Delta and L * log2(e) in the workspace.
  * strides: 24 int64 = (b, h, s) element strides of
  *          q, k, v, o, dout, dq, dk, dv.
  * Preconditions: as the forward, plus n % block_size == 0 (the reference
@@ -97,8 +98,9 @@ int bd3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
 
 /*
  * Backward, first stage: dQ = scale * dS K with dS = P o (dP - Delta),
- * and Delta = rowsum(dO * O) written to `delta` (fp32, contiguous
- * (batch, heads, 2n)) for the second stage.
+ * and, for the second stage, Delta = rowsum(dO * O) and the forward's L
+ * times log2(e) written to `delta`: fp32, contiguous (2, batch, heads, 2n),
+ * plane 0 Delta, plane 1 L * log2(e).
  * strides: 18 int64 = (b, h, s) element strides of q, k, v, o, dout, dq.
  * Preconditions: as bd3_attn_bwd.
  *
@@ -113,7 +115,8 @@ int bd3_attn_bwd_dq(const void* q, const void* k, const void* v,
 
 /*
  * Backward, second stage: dV = P^T dO and dK = scale * dS^T Q, given the
- * Delta the first stage wrote.
+ * two planes (Delta, L * log2(e)) the first stage wrote to `delta`; `lse`
+ * is checked but not read (the kernel uses its base-2 copy).
  * strides: 18 int64 = (b, h, s) element strides of q, k, v, dout, dk, dv.
  * Preconditions: as bd3_attn_bwd.
  *

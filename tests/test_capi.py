@@ -118,7 +118,7 @@ def test_fwd_validation(lib):
 def test_bwd_validation(lib):
     st = _i64([64 * 256, 64 * 256, 64] * 8)
     need = lib.bd3_attn_bwd_workspace_bytes(1, 1, 128, 64)
-    assert need == 1 * 1 * 256 * 4  # Delta
+    assert need == 2 * 1 * 1 * 256 * 4  # Delta and L * log2(e)
     args = [GOOD] * 9
     expect_einval(lib.bd3_attn_bwd(*args, GOOD, need, 1, 1, 128, 64, 3, st, 0.125, None), "multiple of block_size")
     expect_einval(lib.bd3_attn_bwd(*args, GOOD, need - 1, 1, 1, 128, 64, 16, st, 0.125, None), "workspace")
