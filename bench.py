@@ -18,8 +18,10 @@ Printed on stdout as ONE JSON line, with:
                 launches of that kernel); traffic = its HBM bytes per launch from the committed
                 rocprofv3 FETCH_SIZE / WRITE_SIZE summary
                 (profiles/hbm_traffic_pmc.md);
-  cpu_baseline  the fp32 eager oracle's fwd+bwd on the host cores over a
-                bounded sample of (b, h) slices of the same workload;
+  cpu_baseline  the fp32 eager oracle's fwd+bwd (and fwd alone) on the host
+                cores over a bounded sample of (b, h) slices of the same
+                workload; the decode section carries the eager decode
+                oracle's K+V GB/s on the host the same way;
   decode        configs[3]: split-KV decode KV-read GB/s at splits
                 {1, 4, 8, 16}, the reference's default split rule and the
                 auto split, against 8 TB/s;
@@ -220,6 +222,17 @@ def cpu_baseline(B, H, n, bs, budget_s: float):
         if el >= budget_s or done >= B * H:
             break
     flops = 3.5 * useful_fwd_flops(1, 1, n, bs) * done
+    # forward alone (BASELINE's CPU plan times fwd and fwd+bwd)
+    from oracle.attention import bd3_attention
+    with torch.no_grad():
+        bd3_attention(q, k, v, bs)
+        f_done, f0 = 0, time.perf_counter()
+        while True:
+            bd3_attention(q, k, v, bs)
+            f_done += 1
+            f_el = time.perf_counter() - f0
+            if f_el >= budget_s / 3 or f_done >= B * H:
+                break
     cpu_model = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -236,7 +249,36 @@ def cpu_baseline(B, H, n, bs, budget_s: float):
         "sample": (f"{done} of {B * H} (b,h) slices of the B={B} L={n} H={H} bs={bs} workload, "
                    f"fp32 eager fwd+bwd (torch autograd, {cores} threads, {cpu_model}); "
                    f"{el:.1f} s"),
+        "fwd_value": useful_fwd_flops(1, 1, n, bs) * f_done / f_el / 1e12,
+        "fwd_sample": f"{f_done} (b,h) slices, fp32 eager forward only; {f_el:.1f} s",
     }
+
+
+def decode_cpu_baseline(budget_s: float):
+    """The fp32 eager decode oracle on the host cores over (sequence, head)
+    slices of configs[3] (q_len 16 over kv_len 4112) until the budget is
+    spent; value in K+V GB/s (the GPU metric's byte convention)."""
+    import torch
+    from oracle.attention import decode_attention
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    cores = max(1, min(cores, 16))
+    torch.set_num_threads(cores)
+    H, q_len, kv_len, bs = 12, 16, 4112, 16
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(1, H, q_len, D, generator=g).to(torch.bfloat16).float()
+    k, v = (torch.randn(1, H, kv_len, D, generator=g).to(torch.bfloat16).float() for _ in range(2))
+    with torch.no_grad():
+        decode_attention(q, k, v, bs)
+        done, t0 = 0, time.perf_counter()
+        while True:
+            decode_attention(q, k, v, bs)
+            done += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s or done >= 32:
+                break
+    nbytes = 2 * H * kv_len * D * 2 * done
+    return {"value": nbytes / el / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"{done} of 32 sequences (12 heads each) of configs[3], fp32 eager decode; {el:.2f} s"}
 
 
 def decode_bench(device, reps: int):
@@ -588,6 +630,9 @@ def main(argv=None) -> int:
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(B, H, n, bs, args.cpu_budget)
+        if "decode" in result:
+            result["decode"]["cpu_baseline"] = decode_cpu_baseline(args.cpu_budget / 3)
+            log(f"decode cpu baseline: {result['decode']['cpu_baseline']['value']:.1f} GB/s")
         log(f"cpu baseline: {result['cpu_baseline']['value'] * 1e3:.2f} GFLOP/s "
             f"({result['cpu_baseline']['sample']})")
     else:
