@@ -99,14 +99,21 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dkdv_dma_kernel(BwdArgs a) 
   const float* scal_src = ((lane & 16) ? a.delta : a.delta + (int64_t)a.bh * 2 * a.n) + rowbase + 4 * (lane & 15);
   const int64_t qstep = (int64_t)kSwRows * a.sq.s, dostep = (int64_t)kSwRows * a.sdo.s;
   const uint32_t lds0 = lds_addr(&smem[0]);
-  auto issue = [&](int i, int stage) {
-    const int64_t tl = wave_uniform(tile_of(i));
+  // Sources of the next tile to request, walked tile by tile (requests are
+  // made in order: tile_of(0), tile_of(1), ...).
+  TileWalk walk(t0, n_first, t2);
+  TilePtr qn(qp, 2 * qstep, t0, n_first, t2), don(dop, 2 * dostep, t0, n_first, t2);
+  auto issue = [&](int stage) {
     const uint32_t st = lds0 + (uint32_t)(stage * kStageBytes) + (uint32_t)wave * 2048u;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) dma16(qp + tl * qstep, qoff[j], st + 1024u * j);
+    for (int j = 0; j < 2; ++j) dma16(qn.cur, qoff[j], st + 1024u * j);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) dma16(dop + tl * dostep, dooff[j], st + 8192u + 1024u * j);
-    if (wave == 0) dma16_va(scal_src + tl * kSwRows, lds0 + (uint32_t)(stage * kStageBytes) + 16384u);
+    for (int j = 0; j < 2; ++j) dma16(don.cur, dooff[j], st + 8192u + 1024u * j);
+    if (wave == 0) dma16_va(scal_src + walk.tile * kSwRows, lds0 + (uint32_t)(stage * kStageBytes) + 16384u);
+    const bool jumping = walk.left == 1;
+    walk.next();
+    qn.next(jumping);
+    don.next(jumping);
   };
   // Wave 0 has one more load per tile in flight than the others.
   auto wait_barrier = [&](bool in_flight) {
@@ -119,8 +126,8 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dkdv_dma_kernel(BwdArgs a) 
   };
 
   // Tiles 0 and 1 are requested before the K / V rows are waited for.
-  issue(0, 0);
-  if (n_tiles > 1) issue(1, 1);
+  issue(0);
+  if (n_tiles > 1) issue(1);
   // V rows are kept negated: the dP products then start from Delta and give
   // Delta - dP directly (no per-element subtraction), so the kernel forms
   // -dS = P o (Delta - dP) and negates dK once at the end.
@@ -198,7 +205,7 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dkdv_dma_kernel(BwdArgs a) 
   int cur = 0;
   for (int it = 0; it < n_tiles; ++it) {
     const bool pf = it + 2 < n_tiles;
-    if (pf) issue(it + 2, cur == 0 ? 2 : cur - 1);
+    if (pf) issue(cur == 0 ? 2 : cur - 1);
     const int q0 = wave_uniform(tile_of(it) * kSwRows);
     const int c0 = bounds_class(cb, q0, 32, a.n);
     const int c1 = bounds_class(cb, q0 + 32, 32, a.n);
@@ -317,18 +324,24 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dq_dma_kernel(BwdArgs a) {
   }
   const int64_t kstep = (int64_t)kSwRows * a.sk.s, vstep = (int64_t)kSwRows * a.sv.s;
   const uint32_t lds_w = lds_addr(&smem[0][0][0]) + (uint32_t)wave * 2048u;
-  auto issue = [&](int i, int stage) {
-    const int64_t tl = wave_uniform(tile_of(i));
+  // Sources of the next tile to request, walked tile by tile.
+  TileWalk walk(t0, n_first, t2);
+  TilePtr kn(kp, 2 * kstep, t0, n_first, t2), vn(vp, 2 * vstep, t0, n_first, t2);
+  auto issue = [&](int stage) {
     const uint32_t dst = lds_w + (uint32_t)stage * 16384u;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) dma16(kp + tl * kstep, koff[j], dst + 1024u * j);
+    for (int j = 0; j < 2; ++j) dma16(kn.cur, koff[j], dst + 1024u * j);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) dma16(vp + tl * vstep, voff[j], dst + 8192u + 1024u * j);
+    for (int j = 0; j < 2; ++j) dma16(vn.cur, voff[j], dst + 8192u + 1024u * j);
+    const bool jumping = walk.left == 1;
+    walk.next();
+    kn.next(jumping);
+    vn.next(jumping);
   };
 
   // Tiles 0 and 1 are requested before the row loads are waited for.
-  issue(0, 0);
-  if (n_tiles > 1) issue(1, 1);
+  issue(0);
+  if (n_tiles > 1) issue(1);
   // Delta = rowsum(dO o O) (the reference's separate op), stored for dK/dV.
   float dsum = 0.f;
 #pragma unroll
@@ -396,7 +409,7 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dq_dma_kernel(BwdArgs a) {
   int cur = 0;
   for (int it = 0; it < n_tiles; ++it) {
     const bool pf = it + 2 < n_tiles;
-    if (pf) issue(it + 2, cur == 0 ? 2 : cur - 1);
+    if (pf) issue(cur == 0 ? 2 : cur - 1);
     const int k0 = wave_uniform(tile_of(it) * kSwRows);
     const int c0 = bounds_class(cb, k0, 32, a.n);
     const int c1 = bounds_class(cb, k0 + 32, 32, a.n);

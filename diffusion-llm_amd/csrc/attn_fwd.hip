@@ -91,23 +91,28 @@ __global__ __launch_bounds__(256, OCC) void attn_fwd_dma_kernel(FwdArgs a) {
   // LDS byte address of this wave's first K block in stage 0; a stage is
   // 2 * 8 KB (K then V).
   const uint32_t lds_w = lds_addr(&smem[0][0][0]) + (uint32_t)wave * 2048u;
-  auto issue = [&](int i, int stage) {
-    const int64_t tl = wave_uniform(tile_of(i));
-    const uint16_t* kb = kp + tl * kstep;
-    const uint16_t* vb = vp + tl * vstep;
+  // Source of the next tile to request, walked tile by tile (requests are
+  // made in order: tile_of(0), tile_of(1), ...).
+  TileWalk walk(t0, n_first, t2);
+  TilePtr kn(kp, 2 * kstep, t0, n_first, t2), vn(vp, 2 * vstep, t0, n_first, t2);
+  auto issue = [&](int stage) {
     const uint32_t dst = lds_w + (uint32_t)stage * 16384u;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) dma16(kb, koff[j], dst + 1024u * j);
+    for (int j = 0; j < 2; ++j) dma16(kn.cur, koff[j], dst + 1024u * j);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) dma16(vb, voff[j], dst + 8192u + 1024u * j);
+    for (int j = 0; j < 2; ++j) dma16(vn.cur, voff[j], dst + 8192u + 1024u * j);
+    const bool jumping = walk.left == 1;
+    walk.next();
+    kn.next(jumping);
+    vn.next(jumping);
   };
 
   // The first two tiles are requested before waiting for Q, so the two
   // latencies overlap. Consuming Q here (an empty asm reading it) makes the
   // compiler place its own wait for the Q loads at this point; that wait
   // also covers the direct loads issued after them, which is harmless.
-  issue(0, 0);
-  if (n_tiles > 1) issue(1, 1);
+  issue(0);
+  if (n_tiles > 1) issue(1);
 #pragma unroll
   for (int c = 0; c < 4; ++c) asm volatile("" ::"v"(qreg[c]));
   const RowIntervals riv = train_row_intervals(myq, a.n, a.bs);
@@ -122,7 +127,7 @@ __global__ __launch_bounds__(256, OCC) void attn_fwd_dma_kernel(FwdArgs a) {
   int cur = 0;
   for (int it = 0; it < n_tiles; ++it) {
     const bool pf = it + 2 < n_tiles;
-    if (pf) issue(it + 2, cur == 0 ? 2 : cur - 1);
+    if (pf) issue(cur == 0 ? 2 : cur - 1);
     const int k0 = wave_uniform(tile_of(it) * kSwRows);
     const int cls = bounds_class(cb, k0, kSwRows, a.n);
     if (cls != kNone) {

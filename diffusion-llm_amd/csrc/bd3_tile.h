@@ -55,4 +55,32 @@ struct BlockOrder {
   }
 };
 
+// The tiles a workgroup visits are t0 .. t0 + n_first - 1, then t2, t2 + 1,
+// ... (the two live ranges of the schedule; the first may be empty). TileWalk yields, one call per
+// tile, the index and a byte offset scaled by a per-tile stride, by
+// increments instead of a 64-bit multiply per tile (all wave-uniform).
+struct TileWalk {
+  int tile, left, t2;
+  __device__ __forceinline__ TileWalk(int t0_, int n_first, int t2_)
+      : tile(n_first > 0 ? t0_ : t2_), left(n_first), t2(t2_) {}
+  __device__ __forceinline__ void next() {
+    --left;
+    tile = left == 0 ? t2 : tile + 1;
+  }
+};
+
+// A wave-uniform pointer moving along such a walk: `step` bytes per tile,
+// jumping to the second range's first tile when the first range ends.
+struct TilePtr {
+  const char* cur;
+  const char* jump;
+  int64_t step;
+  __device__ __forceinline__ TilePtr(const void* base, int64_t step_bytes, int t0, int n_first, int t2)
+      : cur(static_cast<const char*>(base) + (int64_t)(n_first > 0 ? t0 : t2) * step_bytes),
+        jump(static_cast<const char*>(base) + (int64_t)t2 * step_bytes),
+        step(step_bytes) {}
+  // `jumping`: this step leaves the first range
+  __device__ __forceinline__ void next(bool jumping) { cur = jumping ? jump : cur + step; }
+};
+
 }  // namespace bd3
