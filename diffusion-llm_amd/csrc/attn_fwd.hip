@@ -39,13 +39,21 @@ namespace {
 
 constexpr float kRescale = 8.0f;
 
+#ifndef BD3_FWD_OCC
+#define BD3_FWD_OCC 3
+#endif
+#ifndef BD3_FWD_STAGES
+#define BD3_FWD_STAGES 3
+#endif
+
 // One class per 64-key tile for the wave (dead / full / partial, from the
 // row group's thresholds): a full tile runs straight-line code with no mask
 // arithmetic. MASK16: the block size is a multiple of 16.
 template <int OCC, bool MASK16>
 __global__ __launch_bounds__(256, OCC) void attn_fwd_dma_kernel(FwdArgs a) {
   constexpr int kBM = 128;  // query rows per workgroup: 4 waves x 32
-  constexpr int kStages = 3;
+  constexpr int kStages = BD3_FWD_STAGES;
+  constexpr int kAhead = kStages - 1;  // tiles requested ahead of the one being computed
   __shared__ __attribute__((aligned(1024))) __bf16 smem[kStages][2][kSwTile];  // [stage][K|V]
 
   const int tid = threadIdx.x;
@@ -111,8 +119,9 @@ __global__ __launch_bounds__(256, OCC) void attn_fwd_dma_kernel(FwdArgs a) {
   // latencies overlap. Consuming Q here (an empty asm reading it) makes the
   // compiler place its own wait for the Q loads at this point; that wait
   // also covers the direct loads issued after them, which is harmless.
-  issue(0);
-  if (n_tiles > 1) issue(1);
+#pragma unroll
+  for (int i = 0; i < kAhead; ++i)
+    if (i < n_tiles) issue(i);
 #pragma unroll
   for (int c = 0; c < 4; ++c) asm volatile("" ::"v"(qreg[c]));
   const RowIntervals riv = train_row_intervals(myq, a.n, a.bs);
@@ -126,8 +135,8 @@ __global__ __launch_bounds__(256, OCC) void attn_fwd_dma_kernel(FwdArgs a) {
 
   int cur = 0;
   for (int it = 0; it < n_tiles; ++it) {
-    const bool pf = it + 2 < n_tiles;
-    if (pf) issue(cur == 0 ? 2 : cur - 1);
+    const bool pf = it + kAhead < n_tiles;
+    if (pf) issue(cur + kAhead < kStages ? cur + kAhead : cur + kAhead - kStages);
     const int k0 = wave_uniform(tile_of(it) * kSwRows);
     const int cls = bounds_class(cb, k0, kSwRows, a.n);
     if (cls != kNone) {
@@ -143,13 +152,6 @@ __global__ __launch_bounds__(256, OCC) void attn_fwd_dma_kernel(FwdArgs a) {
       for (int c = 0; c < 4; ++c)
 #pragma unroll
         for (int sb = 0; sb < 2; ++sb) s[sb] = mfma32(kop[sb][c], qreg[c], s[sb]);
-      bf16x8 vop[2][2][2];  // [key block][16-key step][d block]
-#pragma unroll
-      for (int sb = 0; sb < 2; ++sb)
-#pragma unroll
-        for (int kc = 0; kc < 2; ++kc)
-#pragma unroll
-          for (int db = 0; db < 2; ++db) vop[sb][kc][db] = sw_tr_op(vs, 32 * sb + 16 * kc, 32 * db, lane);
 
       // Partial tile: invisible pairs to -inf. With MASK16 (block size a
       // multiple of 16) the mask is constant on 1-row x 16-key strips:
@@ -171,9 +173,16 @@ __global__ __launch_bounds__(256, OCC) void attn_fwd_dma_kernel(FwdArgs a) {
           }
         }
       }
-      float mx = fmaxf(s[0][0], s[1][0]);
+      // Row max over the 32 scores: four independent v_max3 chains.
+      float mq[4];
 #pragma unroll
-      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, fmaxf(s[0][r], s[1][r]));
+      for (int q = 0; q < 4; ++q) {
+        mq[q] = fmaxf(fmaxf(s[0][4 * q], s[0][4 * q + 1]), s[0][4 * q + 2]);
+        mq[q] = fmaxf(fmaxf(mq[q], s[0][4 * q + 3]), s[1][4 * q]);
+        mq[q] = fmaxf(fmaxf(mq[q], s[1][4 * q + 1]), s[1][4 * q + 2]);
+        mq[q] = fmaxf(mq[q], s[1][4 * q + 3]);
+      }
+      const float mx = fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]));
       const float mt = max_xor32(mx) * a.scale_log2;
       if (__ballot(mt > m + kRescale) != 0) {
         const float mn = fmaxf(m, mt);
@@ -198,19 +207,25 @@ __global__ __launch_bounds__(256, OCC) void attn_fwd_dma_kernel(FwdArgs a) {
         }
       }
 #pragma unroll
-      for (int sb = 0; sb < 2; ++sb)
+      for (int sb = 0; sb < 2; ++sb) {
+        bf16x8 vop[2][2];  // V^T operands of key block sb [16-key step][d block], read just before use
 #pragma unroll
         for (int kc = 0; kc < 2; ++kc)
 #pragma unroll
-          for (int db = 0; db < 2; ++db) o[db] = mfma32(vop[sb][kc][db], pop[sb][kc], o[db]);
+          for (int db = 0; db < 2; ++db) vop[kc][db] = sw_tr_op(vs, 32 * sb + 16 * kc, 32 * db, lane);
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+          for (int db = 0; db < 2; ++db) o[db] = mfma32(vop[kc][db], pop[sb][kc], o[db]);
+      }
     }
-    // Tile it+1 complete (the loads of it+2 may stay in flight), and every
-    // wave is done reading stage `cur` before it is refilled.
+    // Tile it+1 complete (the loads of later tiles may stay in flight), and
+    // every wave is done reading stage `cur` before it is refilled.
     if (pf)
-      vm_wait_barrier<4>();
+      vm_wait_barrier<4 * (kAhead - 1)>();
     else
       vm_wait_barrier<0>();
-    cur = cur == 2 ? 0 : cur + 1;
+    cur = cur + 1 == kStages ? 0 : cur + 1;
   }
 
   const float ltot = sum_xor32(lsum);
@@ -228,9 +243,7 @@ __global__ __launch_bounds__(256, OCC) void attn_fwd_dma_kernel(FwdArgs a) {
 
 }  // namespace
 
-#ifndef BD3_FWD_OCC
-#define BD3_FWD_OCC 3
-#endif
+
 
 hipError_t launch_attn_fwd(const FwdArgs& a, hipStream_t stream) {
   // n % 128 == 0 always holds (validated): 128-row query tiles of 4 waves.
