@@ -21,9 +21,7 @@ from types import ModuleType
 import torch
 from torch import Tensor
 
-from kernels.BlockSparseDecodeAttention import block_sparse_decode_attention
-from kernels.BlockSparseFlashAttention import BlockSparseFlashAttention
-from kernels.SplitKVDecodeAttention import split_kv_decode_attention
+import kernels.ops  # noqa: F401  (registers torch.ops.bd3.*)
 
 AttentionFn = Callable[..., Tensor]
 
@@ -31,22 +29,27 @@ FORWARD_RANGE = "attention"
 BACKWARD_RANGE = "attention backward"
 
 
+# The backends call the custom ops (kernels/ops.py), so a caller wrapped in
+# torch.compile traces them without a graph break.
+
+
 def bsfa(q, k, v, mask=None, block_size=None):
     """Block-sparse FlashAttention (forward + backward) on the 2n training
     layout; it builds the mask from block_size."""
-    return BlockSparseFlashAttention.apply(q, k, v, block_size)
+    return torch.ops.bd3.attn_fwd(q, k, v, block_size)[0]
 
 
 def bsdfa(q, k, v, mask=None, block_size=None):
     """Block-sparse decode attention (forward only): the last q_len
     positions, block-causal; it builds the mask from block_size."""
-    return block_sparse_decode_attention(q, k, v, block_size)
+    return torch.ops.bd3.decode(q, k, v, block_size, 0)
 
 
 def split_kv(q, k, v, mask=None, block_size=None):
     """Split-KV decode attention (forward only): bsdfa with the keys split
-    across workgroups, for decode steps with few queries."""
-    return split_kv_decode_attention(q, k, v, block_size)
+    across workgroups, for decode steps with few queries (the reference's
+    split rule)."""
+    return torch.ops.bd3.decode(q, k, v, block_size, -1)
 
 
 BACKENDS: dict[str, AttentionFn] = {
