@@ -35,6 +35,10 @@ Printed on stdout as ONE JSON line, with:
   dit_glue      LayerNorm + adaLN modulate and the gated residual
                 (bd3_ln_modulate, bd3_gate_residual) at configs[1]'s and
                 configs[4]'s shapes against the reference's eager ops;
+  e2e           configs[4]: the restated BD3-LM sampler (8 x 2048 tokens,
+                blocks of 32, 32 steps) with this library on the attention
+                path: tokens/s, the eager path's tokens/s on its first
+                blocks, logit max-abs vs the eager backbone;
   sweep         configs[2]: block sizes {4, 16, 64, 256} at B=4, L=2048,
                 H=16 (useful TFLOP/s and the schedule's useful fraction).
 Human-readable progress goes to stderr.
@@ -539,6 +543,7 @@ def main(argv=None) -> int:
     ap.add_argument("--no-kvcache", action="store_true")
     ap.add_argument("--no-sampling", action="store_true")
     ap.add_argument("--no-glue", action="store_true")
+    ap.add_argument("--no-e2e", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a captured HIP graph")
     args = ap.parse_args(argv)
 
@@ -623,6 +628,14 @@ def main(argv=None) -> int:
                 log(f"dit_glue {k_}: ln_modulate {r['ln_modulate_us']:.1f} us ({r['ln_modulate_GB_s']:.0f} GB/s, "
                     f"eager {r['ln_modulate_reference_eager_us']:.1f} us), gate_residual {r['gate_residual_us']:.1f} us "
                     f"({r['gate_residual_GB_s']:.0f} GB/s, eager {r['gate_residual_reference_eager_us']:.1f} us)")
+    if not args.no_e2e:
+        from perf.e2e_sampling import run as e2e_run
+        result["e2e"] = e2e_run(blocks=64, eager_blocks=2, check_steps=6)
+        worst = max(d["max_abs"] for d in result["e2e"]["logit_check"])
+        log(f"e2e configs[4]: {result['e2e']['tokens_per_s']:.0f} tokens/s "
+            f"(reference eager path {result['e2e']['reference_eager_tokens_per_s']:.0f} tokens/s), "
+            f"logit max-abs vs eager {worst:.4g}")
+        torch.cuda.empty_cache()
     if not args.no_sweep:
         result["sweep"] = sweep_bench(device, steps=10, use_graph=not args.eager)
         for r in result["sweep"]:
