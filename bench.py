@@ -314,6 +314,7 @@ def decode_bench(device, reps: int):
         t = bench(run(eff), warmup=5, rep=reps, flush=True)
         rows.append({"n_splits": eff, "rule": "reference ceil(kv/256)" if ns == 0 else "explicit",
                      "us": t.mean_ms * 1e3, "us_median": t.median_ms * 1e3,
+                     "us_p20": t.p20_ms * 1e3, "us_p80": t.p80_ms * 1e3,
                      "GB_s": kv_bytes / (t.mean_ms * 1e-3) / 1e9})
     # the library's auto split (bd3_decode)
     nb_auto = L.bd3_decode_workspace_bytes(B, H, q_len, kv_len, D, 0)
@@ -325,7 +326,8 @@ def decode_bench(device, reps: int):
                            ptr(ws_auto), nb_auto, stream))
     t = bench(call_auto, warmup=5, rep=reps, flush=True)
     rows.append({"n_splits": auto_splits, "rule": "auto (bd3_decode)", "us": t.mean_ms * 1e3,
-                 "us_median": t.median_ms * 1e3, "GB_s": kv_bytes / (t.mean_ms * 1e-3) / 1e9})
+                 "us_median": t.median_ms * 1e3, "us_p20": t.p20_ms * 1e3, "us_p80": t.p80_ms * 1e3,
+                 "GB_s": kv_bytes / (t.mean_ms * 1e-3) / 1e9})
     best = max(rows, key=lambda r: r["GB_s"])
     return {
         "workload": "split-KV decode, 32 seq x 12 heads, q_len 16, kv_len 4112, d 64, bs 16, bf16",

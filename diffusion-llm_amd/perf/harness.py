@@ -1,9 +1,10 @@
 """Benchmark + correctness harness: bench, check, log_result.
 
 Mirrors the reference's bench/harness.py:25-91 with two MI355X changes:
-  * the cache flush between timed reps zeroes 1 GiB (the reference's 256 MiB,
-    :32-33, does not clear MI355X's 256 MB Infinity Cache on top of the
-    4 MB-per-XCD L2);
+  * the cache flush between timed reps reads 1 GiB (the reference zeroes
+    256 MiB, :32-33, which does not clear MI355X's 256 MB Infinity Cache on
+    top of the 4 MB-per-XCD L2, and a zeroing pass would leave dirty lines
+    whose write-back competes with the timed kernel);
   * timestamps are UTC via timezone.utc (Python 3.10 has no datetime.UTC).
 """
 from __future__ import annotations
