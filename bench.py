@@ -5,8 +5,8 @@
 
 Headline: one step = BD3-LM training attention
 forward + backward (bd3_attn_fwd, bd3_attn_bwd_dq, bd3_attn_bwd_dkdv through
-the C ABI, replayed from one captured HIP graph; --eager launches them one by
-one) at
+the C ABI, launched one after the other on one stream; --graph replays them
+from one captured HIP graph instead) at
 B=8, L=1024 (sequence 2048), H=12, d=64, block 16, bf16, q/k/v/dO ~ N(0,1)
 from seed 0, resident in HBM. value = useful fwd+bwd FLOPs per second:
 3.5 x 4*d*B*H*(n^2 + n*bs) (the reference's convention,
@@ -172,14 +172,27 @@ def _capture_step(step: TrainStep):
         return None
 
 
-def time_train(step: TrainStep, steps: int, warmup: int, use_graph: bool = True):
-    """Warm up, then time exactly `steps` fwd+bwd steps: wall clock between
+def time_train(step: TrainStep, steps: int, warmup: int, use_graph: bool = False, ramp_s: float = 2.0):
+    """Ramp the clocks (eager steps for ramp_s seconds), run `warmup`
+    untimed steps, then time exactly `steps` fwd+bwd steps: wall clock between
     two synchronisations, each step being the forward, dQ and dK/dV launches
-    replayed from one captured HIP graph (or launched eagerly). Separately,
+    on one stream (or replayed from one captured HIP graph: on this stack a
+    freshly captured graph's replays run 5-25% slower than the same launches
+    made directly, for the first few graphs of a process). Separately,
     each kernel's launch duration: HIP events on the launch stream around
     `steps` back-to-back launches of that kernel alone.
     Returns (ms per step, ms per launch of each kernel, launch mode)."""
     import torch
+    # Ramp: on a freshly started process the step runs ~15% slow for the
+    # first ~1.5 s of load (clocks and first touches settling), far longer
+    # than W warm-up steps last. Eager steps for at least ramp_s seconds come
+    # before the W warm-up steps.
+    t_end = time.perf_counter() + ramp_s
+    while time.perf_counter() < t_end:
+        for _ in range(20):
+            step.fwd()
+            step.bwd()
+        torch.cuda.synchronize()
     for _ in range(warmup):
         step.fwd()
         step.bwd()
@@ -514,7 +527,7 @@ def glue_bench(device, reps: int):
     return out
 
 
-def sweep_bench(device, steps: int, use_graph: bool = True):
+def sweep_bench(device, steps: int, use_graph: bool = False):
     """B=4, L=2048, H=16, block sizes {4, 16, 64, 256}."""
     import torch
     from kernels._native import lib
@@ -522,7 +535,7 @@ def sweep_bench(device, steps: int, use_graph: bool = True):
     census = (ctypes.c_int64 * 6)()
     for bs in (4, 16, 64, 256):
         st = TrainStep(4, 16, 2048, bs, device)
-        ms, per, launch = time_train(st, steps, 2, use_graph)
+        ms, per, launch = time_train(st, steps, 2, use_graph, ramp_s=0.3)
         lib().bd3_train_tile_census(2048, bs, census)
         out.append({"block_size": bs, "ms": ms, "launch": launch, "kernel_ms": per,
                     "useful_tflops": st.useful_flops() / (ms * 1e-3) / 1e12,
@@ -546,7 +559,7 @@ def main(argv=None) -> int:
     ap.add_argument("--no-sampling", action="store_true")
     ap.add_argument("--no-glue", action="store_true")
     ap.add_argument("--no-e2e", action="store_true")
-    ap.add_argument("--eager", action="store_true", help="time eager launches instead of a captured HIP graph")
+    ap.add_argument("--graph", action="store_true", help="replay the step from a captured HIP graph instead of launching it")
     args = ap.parse_args(argv)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -563,7 +576,7 @@ def main(argv=None) -> int:
 
     B, H, n, bs = 8, 12, 1024, 16
     step = TrainStep(B, H, n, bs, device)
-    ms, per, launch = time_train(step, args.steps, args.warmup, use_graph=not args.eager)
+    ms, per, launch = time_train(step, args.steps, args.warmup, use_graph=args.graph)
     tflops = step.useful_flops() / (ms * 1e-3) / 1e12
     log(f"config1 fwd+bwd ({launch}): {ms * 1e3:.1f} us/step (fwd {per['fwd'] * 1e3:.1f} us, "
         f"dQ {per['bwd_dq'] * 1e3:.1f} us, dK/dV {per['bwd_dkdv'] * 1e3:.1f} us) -> {tflops:.1f} useful TFLOP/s")
@@ -639,7 +652,7 @@ def main(argv=None) -> int:
             f"logit max-abs vs eager {worst:.4g}")
         torch.cuda.empty_cache()
     if not args.no_sweep:
-        result["sweep"] = sweep_bench(device, steps=10, use_graph=not args.eager)
+        result["sweep"] = sweep_bench(device, steps=10, use_graph=args.graph)
         for r in result["sweep"]:
             log(f"sweep bs={r['block_size']:3d}: {r['ms'] * 1e3:.1f} us, {r['useful_tflops']:.1f} TFLOP/s")
     if not args.no_cpu_baseline:

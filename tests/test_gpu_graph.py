@@ -1,7 +1,7 @@
 """The training step (forward, then backward through bd3_attn_bwd) captured
 as one HIP graph: every replay must equal the eager launches bit for bit
 (the kernels are deterministic), with unrelated eager work and
-synchronisations between the replays. bench.py times the step this way."""
+synchronisations between the replays. bench.py --graph times the step this way."""
 from __future__ import annotations
 
 import pytest
