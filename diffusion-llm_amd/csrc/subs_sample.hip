@@ -219,13 +219,22 @@ __global__ __launch_bounds__(kSubsThreads) void subs_sample_kernel(SubsArgs a) {
       u1 = u53(d[0], d[1]);
     }
   };
-  // Pruning: -log(x) >= 1 - x, so the noise term g = EPS - log(u + EPS) is at
-  // least 1 - u and q / g <= q / (1 - u). An element with q / (1 - u) clearly
-  // below the running best cannot win, so its float64 log and division are
-  // skipped. The margin (1e-6 relative) covers the rounding of the computed
-  // g, whose relative error stays below 1e-10 while 1 - u > 1e-6 (u + EPS is
-  // rounded to 1.1e-16 absolute); elements with 1 - u <= 1e-6 always take the
-  // full path. The chosen token is unchanged.
+  // Pruning: an element whose ratio clearly cannot reach the running best
+  // skips the float64 log and division (the chosen token is unchanged).
+  //  - u < 0.999: g = EPS - log(u + EPS) is estimated in fp32 (relative error
+  //    below 1e-4 there: log's absolute error ~1e-7 against g >= 1e-3), and
+  //    the element is skipped when q < best * g_est * (1 - 2e-4) in fp32;
+  //  - otherwise -log(x) >= 1 - x gives g >= 1 - u, tight as u -> 1, and the
+  //    element is skipped when q < best * (1 - u) * (1 - 1e-6) in float64
+  //    (the margin covers the rounding of u + EPS, 1.1e-16 absolute, while
+  //    1 - u > 1e-6; closer to 1 the element always takes the full path).
+  // The fp32 test compares against the wave's best (any lane's best bounds
+  // the row's winner from below), refreshed after every loop iteration, so
+  // after the first iterations almost no lane of a wave needs the float64
+  // path (a lane-local best would leave some lane on it at nearly every
+  // element position: each lane sees a new record every few elements).
+  float bestf = -INFINITY;  // this lane's best rounded to fp32 (ratios are at most 1e10)
+  float thr = -INFINITY;    // the wave's best at the last refresh
   auto consider = [&](int i, double u) {
     double q;
     if (i == a.mask_index) {
@@ -234,12 +243,19 @@ __global__ __launch_bounds__(kSubsThreads) void subs_sample_kernel(SubsArgs a) {
       const float l = shifted<T>(biased<T>(val(i), i, a.mask_index), m) - lse;
       q = (double)expf(l) * move;
     }
-    const double om = 1.0 - u;
-    if (om > 1e-6 && q < best * om * (1.0 - 1e-6)) return;
+    const float uf = (float)u;
+    if (uf < 0.999f) {
+      const float gf = 1e-10f - __builtin_amdgcn_logf(uf + 1e-10f) * 0.69314718f;
+      if ((float)q < thr * gf * 0.9998f) return;
+    } else {
+      const double om = 1.0 - u;
+      if (om > 1e-6 && q < best * om * (1.0 - 1e-6)) return;
+    }
     const double r = q / (kEps - log(u + kEps));
     if (better(r, i, best, besti)) {
       best = r;
       besti = i;
+      bestf = (float)r;
     }
   };
   // two independent element pairs per iteration
@@ -252,6 +268,10 @@ __global__ __launch_bounds__(kSubsThreads) void subs_sample_kernel(SubsArgs a) {
 #pragma unroll
     for (int h = 0; h < 4; ++h)
       if (idx[h] < V) consider(idx[h], u[h]);
+    float w = bestf;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) w = fmaxf(w, __shfl_xor(w, o, 64));
+    thr = w;
   }
   // argmax across the workgroup
 #pragma unroll
