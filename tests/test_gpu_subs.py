@@ -2,7 +2,8 @@
 against the CPU restatement of the reference (oracle/subs.py): the drawn
 tokens are identical given the same uniforms, both caller-provided and the
 kernel's own Philox4x32-10 stream; masked / unmasked rows, bf16 and fp32
-logits, odd vocabularies, first and last steps; plus the draw's
+logits, odd vocabularies, first and last steps, winners decided below fp32
+resolution and exact ties; plus the draw's
 distribution on the GPU (chi-square)."""
 from __future__ import annotations
 
@@ -79,3 +80,29 @@ def test_distribution_on_gpu(cuda):
     expect = np.append(p * (1 - keep), keep) * n
     chi2 = ((np.bincount(tok, minlength=vocab) - expect) ** 2 / expect).sum()
     assert chi2 < 20.5, chi2
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("vocab,mask", [(VOCAB, MASK), (1001, 0)])
+def test_near_ties_resolved_exactly(cuda, vocab, mask):
+    """Winners decided below fp32 resolution: the pruning filters (an fp32
+    estimate of the Gumbel term for u < 0.999, the 1 - u bound above) must
+    let every contender through to the float64 ratio, and exact ties go to
+    the first index (torch.argmax)."""
+    print(f"subs_sample near ties vocab={vocab}", flush=True)
+    rows, keep = 4, 1e-6  # q = 1e-6 for [MASK], (1 - 1e-6) / (vocab - 1) for every real token
+    logits = torch.zeros(rows, vocab, dtype=torch.bfloat16)
+    xt = torch.full((rows,), mask, dtype=torch.int64)
+    u = torch.full((rows, vocab), 0.25, dtype=torch.float64)
+    a, b = (mask + 100) % vocab, (mask + 200) % vocab
+    u[0, a] = 0.999                                    # the 1 - u branch
+    u[0, b] = np.nextafter(0.999, 1.0)                 # one float64 ulp closer to 1: wins
+    u[1, a] = 0.9                                      # the fp32-estimate branch
+    u[1, b] = 0.9 + 1e-15                              # indistinguishable in fp32: wins
+    u[2, b] = 0.95                                     # exact tie: the first index wins
+    u[2, a] = 0.95
+    u[3, mask] = 1 - 2.0 ** -30                        # [MASK] wins through the 1 - u branch
+    want = orc.sample_step(logits, xt, mask, keep, u)
+    assert want.tolist() == [b, b, min(a, b), mask]
+    got = subs_sample_step(logits.to(cuda), xt.to(cuda), mask, keep, u=u.to(cuda))
+    assert torch.equal(got.cpu(), want)
