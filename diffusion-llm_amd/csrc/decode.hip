@@ -471,11 +471,36 @@ __global__ __launch_bounds__(kThreads) void decode_combine(DecodeArgs a) {
         acc += w * po[s];
       }
     } else {
-      for (int s = 0; s < a.n_splits; ++s) mm = fmaxf(mm, lp[s * kQT]);
-      for (int s = 0; s < a.n_splits; ++s) {
-        const float w = fast_exp2(lp[s * kQT] - mm);
-        wt += w;
-        acc += w * *reinterpret_cast<const f32x4*>(pp + s * kQT * kHeadDim);
+      // Any count, 8 splits per memory round trip (all loads of a group are
+      // issued before the first use); the same weights, summed in split
+      // order.
+      constexpr int kG = 8;
+      const int ns = a.n_splits;
+      for (int s0 = 0; s0 < ns; s0 += kG) {
+        float l[kG];
+#pragma unroll
+        for (int k = 0; k < kG; ++k) l[k] = s0 + k < ns ? lp[(s0 + k) * kQT] : -INFINITY;
+#pragma unroll
+        for (int k = 0; k < kG; ++k) mm = fmaxf(mm, l[k]);
+      }
+      for (int s0 = 0; s0 < ns; s0 += kG) {
+        float l[kG];
+        f32x4 po[kG];
+#pragma unroll
+        for (int k = 0; k < kG; ++k) {
+          if (s0 + k < ns) {
+            l[k] = lp[(s0 + k) * kQT];
+            po[k] = *reinterpret_cast<const f32x4*>(pp + (s0 + k) * kQT * kHeadDim);
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < kG; ++k) {
+          if (s0 + k < ns) {
+            const float w = fast_exp2(l[k] - mm);
+            wt += w;
+            acc += w * po[k];
+          }
+        }
       }
     }
     const float inv = 1.f / wt;
