@@ -108,13 +108,17 @@ bd3::BwdArgs bwd_args(const void* q, const void* k, const void* v, const void* o
 
 int32_t auto_splits(int32_t batch, int32_t heads, int32_t q_len, int32_t kv_len) {
   // At least one workgroup per CU on a 256-CU part; beyond that more splits
-  // only add partial traffic and a merge launch. Never fewer than 128 keys
-  // per split. Measured at configs[3] (384 workgroups at one split): 66 us at
-  // one split, 68 us at two (including the merge), 71 us at three.
+  // only add partial traffic and a merge launch. Never fewer than 512 keys
+  // per split: below that the merge launch costs more than the extra
+  // workgroups gain. Measured at configs[3] (384 workgroups at one split): 66
+  // us at one split, 68 us at two (including the merge), 71 us at three; at
+  // 8 x 12 heads, q_len 32: kv_len 544 12.4 us at one split vs 14.6 at
+  // three, kv_len 1056 16.4 / 16.1 / 16.7 us at one / two / three, kv_len
+  // 2080 24.3 / 20.5 / 21.3 / 20.6 us at one to four.
   const int64_t base = (int64_t)batch * heads * decode_q_tiles(q_len);
   const int64_t target = 256;
   int64_t s = (target + base - 1) / base;
-  const int64_t max_by_len = kv_len / 128 > 0 ? kv_len / 128 : 1;
+  const int64_t max_by_len = kv_len / 512 > 0 ? kv_len / 512 : 1;
   if (s > max_by_len) s = max_by_len;
   if (s < 1) s = 1;
   return (int32_t)s;

@@ -151,7 +151,9 @@ def test_workspace_sizes(lib):
     slots = 2 * 3 * 1 * 4 * 32
     assert lib.bd3_decode_workspace_bytes(2, 3, 16, 100, 64, 4) == slots * 64 * 4 + ((slots * 4 + 255) // 256) * 256
     s = lib.bd3_decode_auto_splits(32, 12, 16, 4112)
-    assert 1 <= s <= 4112 // 128
+    assert s == 1  # 384 workgroups at one split already cover 256 CUs
+    # 96 (b, h) x 1 query tile: enough splits for 256 workgroups, at least 512 keys each
+    assert [lib.bd3_decode_auto_splits(8, 12, 32, kv) for kv in (100, 544, 1056, 2080, 4096)] == [1, 1, 2, 3, 3]
     assert lib.bd3_decode_workspace_bytes(32, 12, 16, 4112, 64, 0) == lib.bd3_decode_workspace_bytes(
         32, 12, 16, 4112, 64, s)
 
