@@ -223,11 +223,15 @@ def generate(cfg, p, tables, batch, n_blocks, steps, backend, check=None, graph=
         g_step = None
         if graph:
             static_block.copy_(block)
-            side = torch.cuda.Stream()
-            side.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(side):
-                backbone_bd3(cfg, p, tables, static_block, cache, False)  # warm-up before capture
-            torch.cuda.current_stream().wait_stream(side)
+            if bi == 0:
+                # Warm-up before the first capture (lazy library state, GEMM
+                # workspaces); later blocks reuse the same shapes but the
+                # cache length, which only changes kernel arguments.
+                side = torch.cuda.Stream()
+                side.wait_stream(torch.cuda.current_stream())
+                with torch.cuda.stream(side):
+                    backbone_bd3(cfg, p, tables, static_block, cache, False)
+                torch.cuda.current_stream().wait_stream(side)
             g_step = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g_step):
                 static_logits = backbone_bd3(cfg, p, tables, static_block, cache, False)
