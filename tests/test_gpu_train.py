@@ -93,6 +93,30 @@ def test_config1_full_size(cuda):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("bs", [4, 16, 64, 256])
+def test_config2_full_size(cuda, bs):
+    """BASELINE config 2 shape (B=4, L=2048, H=16) at each block size of the
+    sweep: forward and backward against the oracle on two (b, h) slices."""
+    B, H, n = 4, 16, 2048
+    print(f"config2 B={B} H={H} n={n} bs={bs}", flush=True)
+    q, k, v, do = train_inputs(B, H, n, seed=bs, count=4)
+    qd, kd, vd, dod = to_dev((q, k, v, do), cuda)
+    o, lse = fwd_capi(qd, kd, vd, bs)
+    dq, dk, dv = bwd_capi(qd, kd, vd, o, dod, lse, bs)
+    torch.cuda.synchronize()
+    for b, h in ((0, 0), (3, 15)):
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        ref_o, ref_lse = bd3_attention(q[sl], k[sl], v[sl], bs)
+        assert max_abs(o[sl], ref_o) <= OUT_TOL
+        assert max_abs(lse[sl], ref_lse) <= LSE_TOL
+        _, rdq, rdk, rdv = bd3_attention_grads(q[sl], k[sl], v[sl], do[sl], bs)
+        for got, ref in ((dq[sl], rdq), (dk[sl], rdk), (dv[sl], rdv)):
+            assert rel_frobenius(got.cpu(), ref) <= GRAD_TOL
+    assert torch.isfinite(o).all() and torch.isfinite(dq).all()
+    assert torch.isfinite(dk).all() and torch.isfinite(dv).all()
+
+
+@pytest.mark.gpu
 def test_strided_v_read_in_place(cuda):
     """q, k, v as views of a fused (B, S, 3, H, d) projection (the model's QKV
     split) give the same result as contiguous copies."""
