@@ -181,15 +181,26 @@ def sample_eager(cfg, logits, block, keep):
 # bd3 backbone: this library's kernels on the attention path
 
 
-def backbone_bd3(cfg, p, tables, block, cache, store):
+def ada_params(cfg, p, B, device):
+    """The adaLN shift / scale / gate vectors of every block and of the
+    final layer (model/modules.py:537-568, :714-716). They depend only on the
+    time conditioning, which is the same for every step of a sampling run
+    (sigma = 0), so the sampler computes them once per run."""
+    c = conditioning(p, B, device)
+    layers = [linear(c, L["ada"]).view(B, 6, 1, cfg.d).unbind(1) for L in p["layers"]]
+    final = linear(c, p["f_ada"]).view(B, 2, 1, cfg.d).unbind(1)
+    return layers, final
+
+
+def backbone_bd3(cfg, p, tables, block, cache, store, ada=None):
     from kernels.dit_glue import gate_residual, ln_modulate
     from kernels.kv_cache import attention_inputs
     B, S = block.shape
     start = cache.length
     x = p["emb"][block]
-    c = conditioning(p, B, block.device)
+    ada_layers, ada_final = ada if ada is not None else ada_params(cfg, p, B, block.device)
     for li, L in enumerate(p["layers"]):
-        sh1, sc1, g1, sh2, sc2, g2 = linear(c, L["ada"]).view(B, 6, 1, cfg.d).unbind(1)
+        sh1, sc1, g1, sh2, sc2, g2 = ada_layers[li]
         h = ln_modulate(x, L["ln1"], sh1, sc1, cfg.eps)
         q, k_all, v_all = attention_inputs(linear(h, L["qkv"]), cfg.heads, *tables, positions=start,
                                            kv_cache=cache, layer_idx=li, store=store)
@@ -197,7 +208,7 @@ def backbone_bd3(cfg, p, tables, block, cache, store):
         x = gate_residual(x, g1, linear(o, L["out"]))
         h = ln_modulate(x, L["ln2"], sh2, sc2, cfg.eps)
         x = gate_residual(x, g2, linear(F.gelu(linear(h, L["fc1"]), approximate="tanh"), L["fc2"]))
-    sh, sc = linear(c, p["f_ada"]).view(B, 2, 1, cfg.d).unbind(1)
+    sh, sc = ada_final
     return linear(ln_modulate(x, p["f_ln"], sh, sc, cfg.eps), p["lm_head"])
 
 
@@ -212,9 +223,11 @@ def generate(cfg, p, tables, batch, n_blocks, steps, backend, check=None, graph=
     from kernels.sampling import PhiloxStream, subs_sample_step
     device = p["emb"].device
     x = torch.empty(batch, 0, device=device, dtype=torch.long)
+    ada = None
     if backend == "bd3":
         cache = KVCache.empty(cfg.layers, capacity=n_blocks * cfg.bs)
         gen = PhiloxStream(seed=0)
+        ada = ada_params(cfg, p, batch, device)
     else:
         cache = [None] * cfg.layers
     static_block = torch.empty((batch, cfg.bs), device=device, dtype=torch.long)
@@ -230,11 +243,11 @@ def generate(cfg, p, tables, batch, n_blocks, steps, backend, check=None, graph=
                 side = torch.cuda.Stream()
                 side.wait_stream(torch.cuda.current_stream())
                 with torch.cuda.stream(side):
-                    backbone_bd3(cfg, p, tables, static_block, cache, False)
+                    backbone_bd3(cfg, p, tables, static_block, cache, False, ada)
                 torch.cuda.current_stream().wait_stream(side)
             g_step = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g_step):
-                static_logits = backbone_bd3(cfg, p, tables, static_block, cache, False)
+                static_logits = backbone_bd3(cfg, p, tables, static_block, cache, False, ada)
         for i in range(steps):
             t, s = 1 - i / steps, 1 - (i + 1) / steps
             if check is not None:
@@ -245,12 +258,15 @@ def generate(cfg, p, tables, batch, n_blocks, steps, backend, check=None, graph=
                     g_step.replay()
                     logits = static_logits
                 else:
-                    logits = backbone_bd3(cfg, p, tables, block, cache, False)
+                    logits = backbone_bd3(cfg, p, tables, block, cache, False, ada)
                 block = subs_sample_step(logits, block, cfg.mask, s / t, generator=gen)
             else:
                 logits = backbone_eager(cfg, p, tables, block, cache, False)
                 block = sample_eager(cfg, logits, block, s / t)
-        (backbone_bd3 if backend == "bd3" else backbone_eager)(cfg, p, tables, block, cache, True)
+        if backend == "bd3":
+            backbone_bd3(cfg, p, tables, block, cache, True, ada)
+        else:
+            backbone_eager(cfg, p, tables, block, cache, True)
         x = torch.cat([x, block], dim=-1)
         del g_step
     return x
