@@ -486,9 +486,10 @@ def glue_bench(device, reps: int):
     result for the next matmul) and configs[4]'s sampling step (8 x 32
     tokens, all bf16): bd3_ln_modulate and bd3_gate_residual against the
     reference's eager ops on the same GPU (model/modules.py:243-288,
-    :778-788, :560-566). HIP events, 1 GiB cache flush before each rep."""
+    :778-788, :560-566), and the two fused (bd3_gate_residual_ln_modulate).
+    HIP events, 1 GiB cache flush before each rep."""
     import torch
-    from kernels.dit_glue import gate_residual, ln_modulate
+    from kernels.dit_glue import gate_residual, gate_residual_ln_modulate, ln_modulate
     from perf.harness import bench
     out = {}
     for name, (B, S, xd) in (("training", (8, 2048, torch.float32)), ("sampling_step", (8, 32, torch.bfloat16))):
@@ -510,6 +511,8 @@ def glue_bench(device, reps: int):
         t_ln_e = bench(eager_ln, warmup=3, rep=reps, flush=True)
         t_gr = bench(lambda: gate_residual(x, gt, y), warmup=3, rep=reps, flush=True)
         t_gr_e = bench(lambda: x + gt * y, warmup=3, rep=reps, flush=True)
+        t_fu = bench(lambda: gate_residual_ln_modulate(x, gt, y, w, sh, sc, out_dtype=torch.bfloat16), warmup=3,
+                     rep=reps, flush=True)
         xb = x.element_size()
         ln_bytes = B * S * D * (xb + 2)            # x read, bf16 result written
         gr_bytes = B * S * D * (2 * xb + 2)        # x and y read, result (x's dtype) written
@@ -517,7 +520,8 @@ def glue_bench(device, reps: int):
                      "ln_modulate_us": t_ln.median_ms * 1e3, "ln_modulate_reference_eager_us": t_ln_e.median_ms * 1e3,
                      "ln_modulate_GB_s": ln_bytes / (t_ln.median_ms * 1e-3) / 1e9,
                      "gate_residual_us": t_gr.median_ms * 1e3, "gate_residual_reference_eager_us": t_gr_e.median_ms * 1e3,
-                     "gate_residual_GB_s": gr_bytes / (t_gr.median_ms * 1e-3) / 1e9}
+                     "gate_residual_GB_s": gr_bytes / (t_gr.median_ms * 1e-3) / 1e9,
+                     "gate_residual_ln_modulate_us": t_fu.median_ms * 1e3}
         del x, y
         torch.cuda.empty_cache()
     tr = out["training"]
@@ -642,7 +646,8 @@ def main(argv=None) -> int:
             if k_ != "roofline":
                 log(f"dit_glue {k_}: ln_modulate {r['ln_modulate_us']:.1f} us ({r['ln_modulate_GB_s']:.0f} GB/s, "
                     f"eager {r['ln_modulate_reference_eager_us']:.1f} us), gate_residual {r['gate_residual_us']:.1f} us "
-                    f"({r['gate_residual_GB_s']:.0f} GB/s, eager {r['gate_residual_reference_eager_us']:.1f} us)")
+                    f"({r['gate_residual_GB_s']:.0f} GB/s, eager {r['gate_residual_reference_eager_us']:.1f} us), "
+                    f"fused {r['gate_residual_ln_modulate_us']:.1f} us")
     if not args.no_e2e:
         from perf.e2e_sampling import run as e2e_run
         result["e2e"] = e2e_run(blocks=64, eager_blocks=2, check_steps=6)

@@ -116,9 +116,11 @@ struct GlueArgs {
   const void* scale;   // (batch, d)
   const void* y;       // (batch, seq, d) sublayer output (gate_residual)
   void* out;
+  const void* gate;    // (batch, d) gate of the fused residual + LayerNorm (stride sm_b)
+  void* out_x;         // (batch, seq, d) updated residual of the fused form
   int x_fp32, w_fp32, m_fp32, y_fp32, out_fp32;
   int rows, seq, d;
-  int64_t sx_b, sx_s, sm_b, sy_b, sy_s, so_b, so_s;  // element strides
+  int64_t sx_b, sx_s, sm_b, sy_b, sy_s, so_b, so_s, sxo_b, sxo_s;  // element strides
   float eps;
 };
 
@@ -130,6 +132,7 @@ hipError_t launch_qkv_rope(const QkvRopeArgs& a, hipStream_t stream);
 hipError_t launch_kv_write(const KvWriteArgs& a, hipStream_t stream);
 hipError_t launch_subs_sample(const SubsArgs& a, hipStream_t stream);
 hipError_t launch_ln_modulate(const GlueArgs& a, hipStream_t stream);
+hipError_t launch_gate_residual_ln_modulate(const GlueArgs& a, hipStream_t stream);
 hipError_t launch_gate_residual(const GlueArgs& a, hipStream_t stream);
 hipError_t launch_mask_dump(uint8_t* out, int mode, int rows, int kv_len,
                             int bs, hipStream_t stream);

@@ -487,6 +487,35 @@ int bd3_gate_residual(const void* x, int32_t x_fp32, const void* gate, int32_t g
   return hip_status(bd3::launch_gate_residual(a, static_cast<hipStream_t>(stream)), "gate_residual launch");
 }
 
+int bd3_gate_residual_ln_modulate(const void* x, int32_t x_fp32, const void* gate, const void* y,
+                                  int32_t y_fp32, void* x_out, const void* weight,
+                                  int32_t weight_fp32, const void* shift, const void* scale,
+                                  int32_t mod_fp32, void* out, int32_t out_fp32, int32_t batch,
+                                  int32_t seq, int32_t d_model, const int64_t* strides, float eps,
+                                  void* stream) {
+  const int32_t flags[5] = {x_fp32, y_fp32, weight_fp32, mod_fp32, out_fp32};
+  int st = check_glue_common(batch, seq, d_model, strides, 9, flags, 5);
+  if (st) return st;
+  const void* ptrs[8] = {x, gate, y, x_out, weight, shift, scale, out};
+  const char* names[8] = {"x", "gate", "y", "x_out", "weight", "shift", "scale", "out"};
+  if ((st = check_ptrs(ptrs, names, 8))) return st;
+  const bool res_bf16 = !x_fp32 && !mod_fp32 && !y_fp32;
+  if (res_bf16 && !mod_fp32 && out_fp32)
+    return fail(BD3_EINVAL, "bf16 x_out with bf16 shift / scale modulates in bf16: out must be bf16");
+  if (!(eps >= 0.f)) return fail(BD3_EINVAL, "eps must be >= 0");
+  if (d_model > 4096) return fail(BD3_EINVAL, "d_model must be <= 4096, got %d", d_model);
+  bd3::GlueArgs a = {};
+  a.x = x; a.gate = gate; a.y = y; a.out_x = x_out;
+  a.weight = weight; a.shift = shift; a.scale = scale; a.out = out;
+  a.x_fp32 = x_fp32; a.y_fp32 = y_fp32; a.w_fp32 = weight_fp32; a.m_fp32 = mod_fp32; a.out_fp32 = out_fp32;
+  a.rows = batch * seq; a.seq = seq > 0 ? seq : 1; a.d = d_model;
+  a.sx_b = strides[0]; a.sx_s = strides[1]; a.sm_b = strides[2]; a.sy_b = strides[3]; a.sy_s = strides[4];
+  a.sxo_b = strides[5]; a.sxo_s = strides[6]; a.so_b = strides[7]; a.so_s = strides[8];
+  a.eps = eps;
+  return hip_status(bd3::launch_gate_residual_ln_modulate(a, static_cast<hipStream_t>(stream)),
+                    "gate_residual_ln_modulate launch");
+}
+
 int bd3_mask_dump(uint8_t* out, int32_t mode, int32_t rows, int32_t kv_len, int32_t block_size,
                   void* stream) {
   if (out == nullptr) return fail(BD3_EINVAL, "out is NULL");

@@ -52,6 +52,9 @@ SIGNATURES: dict[str, tuple] = {
     "bd3_ln_modulate": (ctypes.c_int, [_c_p, _i32, _c_p, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32, _i32, _i32,
                                        _i64p, _f32, _c_p]),
     "bd3_gate_residual": (ctypes.c_int, [_c_p, _i32, _c_p, _i32, _c_p, _i32, _c_p, _i32, _i32, _i32, _i64p, _c_p]),
+    "bd3_gate_residual_ln_modulate": (ctypes.c_int, [_c_p, _i32, _c_p, _c_p, _i32, _c_p, _c_p, _i32, _c_p, _c_p,
+                                                     _i32, _c_p, _i32, _i32, _i32, _i32, _i64p, _f32,
+                                                     _c_p]),
     "bd3_mask_dump": (ctypes.c_int, [_c_p, _i32, _i32, _i32, _i32, _c_p]),
     "bd3_train_tile_census": (ctypes.c_int, [_i32, _i32, _i64p]),
     "bd3_train_classify": (ctypes.c_int, [_i32, _i32, _i32, _i32]),

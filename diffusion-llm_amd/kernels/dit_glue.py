@@ -66,3 +66,31 @@ def gate_residual(x: Tensor, gate: Tensor, y: Tensor, out: Tensor | None = None)
     check(lib().bd3_gate_residual(ptr(x), _F[x.dtype], ptr(gate), _F[gate.dtype], ptr(y), _F[y.dtype],
                                   ptr(out), B, S, D, st, stream_of(x)))
     return out
+
+
+def gate_residual_ln_modulate(x: Tensor, gate: Tensor, y: Tensor, weight: Tensor, shift: Tensor,
+                              scale: Tensor, eps: float = 1e-5, out_dtype: torch.dtype | None = None,
+                              x_out: Tensor | None = None) -> tuple[Tensor, Tensor]:
+    """(x + gate * y, modulate(LN(x + gate * y), shift, scale)) in one launch,
+    bit-exact with gate_residual followed by ln_modulate; `x_out=x` updates
+    the residual in place."""
+    assert x.dim() == 3 and x.shape == y.shape and x.is_cuda
+    B, S, D = x.shape
+    x, y, weight = _ready(x), _ready(y), _ready(weight)
+    gate, shift, scale = _vec(gate), _vec(shift), _vec(scale)
+    assert gate.dtype == shift.dtype == scale.dtype and gate.shape == shift.shape == scale.shape == (B, D)
+    if not gate.stride(0) == shift.stride(0) == scale.stride(0):  # one batch stride for the three
+        gate, shift, scale = gate.contiguous(), shift.contiguous(), scale.contiguous()
+    res = torch.bfloat16 if x.dtype == gate.dtype == y.dtype == torch.bfloat16 else torch.float32
+    if x_out is None:
+        x_out = torch.empty((B, S, D), device=x.device, dtype=res)
+    assert x_out.dtype == res and x_out.shape == x.shape
+    natural = torch.bfloat16 if (res == torch.bfloat16 and shift.dtype == torch.bfloat16) else torch.float32
+    out = torch.empty((B, S, D), device=x.device, dtype=out_dtype or natural)
+    st = (ctypes.c_int64 * 9)(x.stride(0), x.stride(1), gate.stride(0), y.stride(0), y.stride(1),
+                              x_out.stride(0), x_out.stride(1), out.stride(0), out.stride(1))
+    check(lib().bd3_gate_residual_ln_modulate(ptr(x), _F[x.dtype], ptr(gate), ptr(y), _F[y.dtype], ptr(x_out),
+                                              ptr(weight), _F[weight.dtype], ptr(shift), ptr(scale),
+                                              _F[shift.dtype], ptr(out), _F[out.dtype], B, S, D, st, float(eps),
+                                              stream_of(x)))
+    return x_out, out

@@ -193,23 +193,29 @@ def ada_params(cfg, p, B, device):
 
 
 def backbone_bd3(cfg, p, tables, block, cache, store, ada=None):
-    from kernels.dit_glue import gate_residual, ln_modulate
+    from kernels.dit_glue import gate_residual_ln_modulate, ln_modulate
     from kernels.kv_cache import attention_inputs
     B, S = block.shape
     start = cache.length
     x = p["emb"][block]
     ada_layers, ada_final = ada if ada is not None else ada_params(cfg, p, B, block.device)
-    for li, L in enumerate(p["layers"]):
-        sh1, sc1, g1, sh2, sc2, g2 = ada_layers[li]
-        h = ln_modulate(x, L["ln1"], sh1, sc1, cfg.eps)
+    layers = p["layers"]
+    sh1, sc1 = ada_layers[0][0], ada_layers[0][1]
+    h = ln_modulate(x, layers[0]["ln1"], sh1, sc1, cfg.eps)
+    for li, L in enumerate(layers):
+        _, _, g1, sh2, sc2, g2 = ada_layers[li]
         q, k_all, v_all = attention_inputs(linear(h, L["qkv"]), cfg.heads, *tables, positions=start,
                                            kv_cache=cache, layer_idx=li, store=store)
         o = torch.ops.bd3.decode(q, k_all, v_all, cfg.bs, 0).transpose(1, 2).reshape(B, S, cfg.d)
-        x = gate_residual(x, g1, linear(o, L["out"]))
-        h = ln_modulate(x, L["ln2"], sh2, sc2, cfg.eps)
-        x = gate_residual(x, g2, linear(F.gelu(linear(h, L["fc1"]), approximate="tanh"), L["fc2"]))
-    sh, sc = ada_final
-    return linear(ln_modulate(x, p["f_ln"], sh, sc, cfg.eps), p["lm_head"])
+        # each residual update fused with the LayerNorm + modulate that reads it next
+        x, h = gate_residual_ln_modulate(x, g1, linear(o, L["out"]), L["ln2"], sh2, sc2, cfg.eps)
+        y = linear(F.gelu(linear(h, L["fc1"]), approximate="tanh"), L["fc2"])
+        if li + 1 < len(layers):
+            w_next, (sh_next, sc_next) = layers[li + 1]["ln1"], ada_layers[li + 1][:2]
+        else:
+            w_next, (sh_next, sc_next) = p["f_ln"], ada_final
+        x, h = gate_residual_ln_modulate(x, g2, y, w_next, sh_next, sc_next, cfg.eps)
+    return linear(h, p["lm_head"])
 
 
 def generate(cfg, p, tables, batch, n_blocks, steps, backend, check=None, graph=False):

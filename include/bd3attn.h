@@ -295,6 +295,27 @@ int bd3_gate_residual(const void* x, int32_t x_fp32, const void* gate, int32_t g
                       int32_t d_model, const int64_t* strides, void* stream);
 
 /*
+ * The two above fused, as DiTBlock.forward chains them (model/modules.py:
+ * 560-566, then the next sublayer's :537-568): x_out = x + gate * y with
+ * bd3_gate_residual's dtypes and roundings, then out = modulate(LN(x_out),
+ * shift, scale) with bd3_ln_modulate's, x_out's dtype as the LayerNorm
+ * input's. One launch and one read of the residual instead of two of each;
+ * bit-exact with the two calls in sequence. x_out may alias x.
+ *   x, y, x_out, out: (batch, seq, d_model); gate, shift, scale:
+ *   (batch, d_model), all of dtype mod_fp32; weight: (d_model).
+ *   x_out's dtype is bf16 when x, y and the vectors all are, else fp32.
+ *   strides: 9 element strides: x (batch, seq), gate / shift / scale
+ *   (batch), y (batch, seq), x_out (batch, seq), out (batch, seq); same
+ *   alignment rules and d_model limit as bd3_ln_modulate.
+ */
+int bd3_gate_residual_ln_modulate(const void* x, int32_t x_fp32, const void* gate, const void* y,
+                                  int32_t y_fp32, void* x_out, const void* weight,
+                                  int32_t weight_fp32, const void* shift, const void* scale,
+                                  int32_t mod_fp32, void* out, int32_t out_fp32, int32_t batch,
+                                  int32_t seq, int32_t d_model, const int64_t* strides, float eps,
+                                  void* stream);
+
+/*
  * Writes the mask the device predicate applies, one byte per (row, key)
  * (1 = may attend), row-major:
  *   mode 0 (training): (2n, 2n) with n = rows, kv_len ignored;

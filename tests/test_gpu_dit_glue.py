@@ -1,5 +1,7 @@
-"""GPU parity of the fused DiT glue (bd3_ln_modulate, bd3_gate_residual)
-against oracle/dit.py: the gated residual bit-exact in every dtype mix;
+"""GPU parity of the fused DiT glue (bd3_ln_modulate, bd3_gate_residual,
+bd3_gate_residual_ln_modulate) against oracle/dit.py: the gated residual
+bit-exact in every dtype mix; the residual + LayerNorm fusion bit-exact with
+the two calls it replaces;
 LayerNorm + modulate within the rounding its fp32 row statistics allow
 (summation order differs): fp32 results within 1e-5 relative, bf16 results
 within one bf16 ulp per rounding of the magnitudes entering the last add, at most 1% of
@@ -65,3 +67,37 @@ def test_gate_residual_in_place(cuda):
     want = ref_gate(x.cpu(), g.cpu(), y.cpu())
     out = gate_residual(x, g, y, out=x)
     assert out.data_ptr() == x.data_ptr() and torch.equal(x.cpu(), want)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("xd,md,yd,od", [(BF, BF, BF, BF), (F32, BF, BF, None), (F32, BF, BF, BF),
+                                         (BF, F32, BF, None), (F32, F32, F32, None)])
+@pytest.mark.parametrize("B,S,D", [(2, 37, 768), (1, 5, 64), (3, 2, 4096)])
+def test_gate_residual_ln_modulate_matches_two_calls(cuda, xd, md, yd, od, B, S, D):
+    """The fused residual + LayerNorm + modulate equals gate_residual followed
+    by ln_modulate bit for bit (same kernels' arithmetic, one launch), both
+    outputs, including the in-place residual update; vectors sliced from one
+    (batch, 6, 1, d) adaLN tensor as the model does."""
+    from kernels.dit_glue import gate_residual_ln_modulate
+    print(f"gate_residual_ln_modulate x={xd} mod={md} y={yd} out={od} shape=({B},{S},{D})", flush=True)
+    x = rnd((B, S, D), xd, 11, scale=2.0, shift=0.3).to(cuda)
+    y = rnd((B, S, D), yd, 12).to(cuda)
+    ada = rnd((B, 6, 1, D), md, 13, 0.5).to(cuda)
+    g, sh, sc = ada[:, 2], ada[:, 3], ada[:, 4]
+    w = rnd((D,), F32, 14, scale=0.2, shift=1.0).to(cuda)
+    want_x = gate_residual(x, g, y)
+    want_h = ln_modulate(want_x, w, sh, sc, out_dtype=od)
+    got_x, got_h = gate_residual_ln_modulate(x, g, y, w, sh, sc, out_dtype=od)
+    assert got_x.dtype == want_x.dtype and got_h.dtype == want_h.dtype
+    assert torch.equal(got_x, want_x) and torch.equal(got_h, want_h)
+    if got_x.dtype == x.dtype:  # in place
+        x2 = x.clone()
+        got_x2, got_h2 = gate_residual_ln_modulate(x2, g, y, w, sh, sc, out_dtype=od, x_out=x2)
+        assert got_x2.data_ptr() == x2.data_ptr()
+        assert torch.equal(x2, want_x) and torch.equal(got_h2, want_h)
+    # gate and the modulation vectors from different adaLN tensors (the last
+    # layer's gate with the final layer's shift / scale): batch strides differ
+    fin = rnd((B, 2, 1, D), md, 15, 0.5).to(cuda)
+    want_h3 = ln_modulate(want_x, w, fin[:, 0], fin[:, 1], out_dtype=od)
+    _, got_h3 = gate_residual_ln_modulate(x, g, y, w, fin[:, 0], fin[:, 1], out_dtype=od)
+    assert torch.equal(got_h3, want_h3)
