@@ -221,3 +221,17 @@ def test_dit_glue_validation(lib):
     expect_einval(gr(g=None), "gate is NULL")
     expect_einval(gr(d=0), "multiple of 8")
     expect_einval(gr(st=None), "strides is NULL")
+
+
+def test_fused_glue_validation(lib):
+    st9 = _i64([768 * 16, 768, 768 * 6, 768 * 16, 768, 768 * 16, 768, 768 * 16, 768])
+    fu = lambda **kw: lib.bd3_gate_residual_ln_modulate(
+        GOOD, kw.get("xf", 0), kw.get("g", GOOD), GOOD, kw.get("yf", 0), kw.get("xo", GOOD), GOOD, 1, GOOD, GOOD,
+        kw.get("mf", 0), GOOD, kw.get("of", 0), 2, 16, kw.get("d", 768), kw.get("st", st9), kw.get("eps", 1e-5), None)
+    expect_einval(fu(g=None), "gate is NULL")
+    expect_einval(fu(xo=GOOD + 8), "x_out must be 16-byte aligned")
+    expect_einval(fu(d=4104), "d_model must be <= 4096")
+    expect_einval(fu(of=1), "out must be bf16")   # all bf16: modulates in bf16
+    expect_einval(fu(yf=3), "dtype flags")
+    expect_einval(fu(eps=float("nan")), "eps")
+    expect_einval(fu(st=_i64([768 * 16, 768, 768 * 6, 768 * 16, 768, 768 * 16, 769, 768 * 16, 768])), "stride[6]")
