@@ -134,6 +134,11 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dkdv_dma_kernel(BwdArgs a) 
 #pragma unroll
   for (int c = 0; c < 4; ++c)
     vreg[c] = __builtin_bit_cast(bf16x8, __builtin_bit_cast(u32x4, vreg[c]) ^ 0x80008000u);
+  // K is held times -scale * log2(e) (rounded to bf16) and the score chains
+  // start from the rows' L * log2(e), so they give minus the base-2 exponent
+  // of P (negated for free by the exp's input modifier).
+#pragma unroll
+  for (int c = 0; c < 4; ++c) kreg[c] = scale_bf16x8(kreg[c], -a.scale_log2);
 #pragma unroll
   for (int c = 0; c < 4; ++c) asm volatile("" ::"v"(kreg[c]), "v"(vreg[c]));
   const RowIntervals civ = train_col_intervals(key, a.n, a.bs);
@@ -156,27 +161,27 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dkdv_dma_kernel(BwdArgs a) 
       qa[c] = sw_row_op(qs, 32 * qb, c, lane);
       da[c] = sw_row_op(dos, 32 * qb, c, lane);
     }
-    // Delta of the rows, in accumulator order, as the start of the dP chain.
-    f32x16 dp;
+    // The rows' Delta and L * log2(e), in accumulator order, as the starts
+    // of the dP and score chains.
+    f32x16 dp, s;
 #pragma unroll
     for (int rg = 0; rg < 4; ++rg) {
       const f32x4 dr = *reinterpret_cast<const f32x4*>(&scal[64 + 32 * qb + 8 * rg + 4 * g]);
+      const f32x4 lr = *reinterpret_cast<const f32x4*>(&scal[32 * qb + 8 * rg + 4 * g]);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) dp[4 * rg + j] = dr[j];
+      for (int j = 0; j < 4; ++j) {
+        dp[4 * rg + j] = dr[j];
+        s[4 * rg + j] = lr[j];
+      }
     }
-    f32x16 s = {};
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      s = mfma32(qa[c], kreg[c], s);
+      s = mfma32(qa[c], kreg[c], s);     // L * log2(e) - S * scale * log2(e)
       dp = mfma32(da[c], vreg[c], dp);  // Delta - dP (V negated)
     }
     float p[16];
 #pragma unroll
-    for (int rg = 0; rg < 4; ++rg) {
-      const f32x4 lr = *reinterpret_cast<const f32x4*>(&scal[32 * qb + 8 * rg + 4 * g]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) p[4 * rg + j] = fast_exp2(fmaf(s[4 * rg + j], a.scale_log2, -lr[j]));
-    }
+    for (int r = 0; r < 16; ++r) p[r] = fast_exp2(-s[r]);
     if (masked) {
       if (MASK16) {
         const bool lo = iv_has(civ, q0 + 32 * qb), hi = iv_has(civ, q0 + 32 * qb + 16);

@@ -28,6 +28,8 @@
 // is updated lazily: O and l are rescaled only when some row's max grew by
 // more than kRescale (log2 units); otherwise the stale max is kept, which
 // bounds P by 2^kRescale and leaves O / l exact.
+#include <type_traits>
+
 #include "bd3_device.h"
 #include "bd3_launch.h"
 #include "bd3_mask.h"
@@ -41,6 +43,9 @@ constexpr float kRescale = 8.0f;
 
 #ifndef BD3_FWD_OCC
 #define BD3_FWD_OCC 3
+#endif
+#ifndef BD3_FWD_HALF
+#define BD3_FWD_HALF 0
 #endif
 #ifndef BD3_FWD_STAGES
 #define BD3_FWD_STAGES 3
@@ -122,13 +127,114 @@ __global__ __launch_bounds__(256, OCC) void attn_fwd_dma_kernel(FwdArgs a) {
 #pragma unroll
   for (int i = 0; i < kAhead; ++i)
     if (i < n_tiles) issue(i);
+  // Q times scale * log2(e), rounded to bf16: K Q'^T is then the base-2
+  // exponent, and a chain started from -m gives S * scale * log2(e) - m.
 #pragma unroll
-  for (int c = 0; c < 4; ++c) asm volatile("" ::"v"(qreg[c]));
+  for (int c = 0; c < 4; ++c) qreg[c] = scale_bf16x8(qreg[c], a.scale_log2);
   const RowIntervals riv = train_row_intervals(myq, a.n, a.bs);
   const ClassBounds cb = uniform_bounds(row_group_bounds(train_row_group(qrow0, 32, a.n, a.bs), a.n));
 
   f32x16 o[2] = {};  // O^T [d block]
-  float m = -INFINITY, lsum = 0.f;
+  // mref: the row's reference maximum (log2 units); the score chains start
+  // from negm = -mref. `valid` once the row has met a live key.
+  float mref = 0.f, lsum = 0.f;
+  bool valid = false;
+  f32x16 negm = {};
+
+  // One tile step over NSB 32-key halves of the current 64-key tile,
+  // starting at half sb0 (NSB = 1: the other half is dead for this wave).
+  auto step = [&](auto nsb_c, int sb0, int k0, int cls, const __bf16* ks, const __bf16* vs) {
+    constexpr int NSB = decltype(nsb_c)::value;
+    bf16x8 kop[NSB][4];
+#pragma unroll
+    for (int sb = 0; sb < NSB; ++sb)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) kop[sb][c] = sw_row_op(ks, 32 * (sb0 + sb), c, lane);
+    f32x16 s[NSB];
+#pragma unroll
+    for (int sb = 0; sb < NSB; ++sb) s[sb] = mfma32(kop[sb][0], qreg[0], negm);
+#pragma unroll
+    for (int c = 1; c < 4; ++c)
+#pragma unroll
+      for (int sb = 0; sb < NSB; ++sb) s[sb] = mfma32(kop[sb][c], qreg[c], s[sb]);
+
+    // Partial tile: invisible pairs to -inf. With MASK16 (block size a
+    // multiple of 16) the mask is constant on 1-row x 16-key strips:
+    // registers 0-7 of a key block hold its keys 0-15, registers 8-15 keys
+    // 16-31, so one test per strip decides them.
+    if (cls == kPartial) {
+#pragma unroll
+      for (int sb = 0; sb < NSB; ++sb) {
+        const int kb = k0 + 32 * (sb0 + sb);
+        if (MASK16) {
+          const bool lo = iv_has(riv, kb), hi = iv_has(riv, kb + 16);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[sb][r] = (r < 8 ? lo : hi) ? s[sb][r] : -INFINITY;
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = kb + 8 * (r >> 2) + 4 * g + (r & 3);
+            s[sb][r] = iv_has(riv, key) ? s[sb][r] : -INFINITY;
+          }
+        }
+      }
+    }
+    // Row max of the shifted scores: four independent v_max3 chains.
+    float mq[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      mq[q] = fmaxf(fmaxf(s[0][4 * q], s[0][4 * q + 1]), s[0][4 * q + 2]);
+      mq[q] = fmaxf(mq[q], s[0][4 * q + 3]);
+#pragma unroll
+      for (int sb = 1; sb < NSB; ++sb) {
+        mq[q] = fmaxf(fmaxf(mq[q], s[sb][4 * q]), s[sb][4 * q + 1]);
+        mq[q] = fmaxf(fmaxf(mq[q], s[sb][4 * q + 2]), s[sb][4 * q + 3]);
+      }
+    }
+    const float mt = max_xor32(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3])));
+    // A new reference when the row had none (and this tile has a live key)
+    // or its maximum grew by more than kRescale: the scores shift by delta,
+    // O and l scale by 2^-delta.
+    if (__ballot(!valid || mt > kRescale) != 0) {
+      const float delta = valid ? fmaxf(mt, 0.f) : (mt == -INFINITY ? 0.f : mt);
+      const float alpha = valid ? fast_exp2(-delta) : 1.f;
+      valid = valid || mt != -INFINITY;
+      mref += delta;
+      negm = splat16(-mref);
+#pragma unroll
+      for (int sb = 0; sb < NSB; ++sb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[sb][r] -= delta;
+      lsum *= alpha;
+      o[0] *= alpha;
+      o[1] *= alpha;
+    }
+    bf16x8 pop[NSB][2];  // P^T operands [key block][16-key step]
+#pragma unroll
+    for (int sb = 0; sb < NSB; ++sb) {
+      float p[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) p[r] = fast_exp2(s[sb][r]);
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) {
+        pop[sb][kc] = to_bf16x8(p[8 * kc], p[8 * kc + 1], p[8 * kc + 2], p[8 * kc + 3], p[8 * kc + 4],
+                                p[8 * kc + 5], p[8 * kc + 6], p[8 * kc + 7]);
+        lsum = sum_bf16x8(pop[sb][kc], lsum);
+      }
+    }
+#pragma unroll
+    for (int sb = 0; sb < NSB; ++sb) {
+      bf16x8 vop[2][2];  // V^T operands of key block sb [16-key step][d block], read just before use
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+        for (int db = 0; db < 2; ++db) vop[kc][db] = sw_tr_op(vs, 32 * (sb0 + sb) + 16 * kc, 32 * db, lane);
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+        for (int db = 0; db < 2; ++db) o[db] = mfma32(vop[kc][db], pop[sb][kc], o[db]);
+    }
+  };
 
   // Every row group sees at least its own block, so n_tiles >= 1.
   vm_wait_barrier<0>();
@@ -138,87 +244,21 @@ __global__ __launch_bounds__(256, OCC) void attn_fwd_dma_kernel(FwdArgs a) {
     const bool pf = it + kAhead < n_tiles;
     if (pf) issue(cur + kAhead < kStages ? cur + kAhead : cur + kAhead - kStages);
     const int k0 = wave_uniform(tile_of(it) * kSwRows);
-    const int cls = bounds_class(cb, k0, kSwRows, a.n);
-    if (cls != kNone) {
-      const __bf16* ks = smem[cur][0];
-      const __bf16* vs = smem[cur][1];
-      bf16x8 kop[2][4];
-#pragma unroll
-      for (int sb = 0; sb < 2; ++sb)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) kop[sb][c] = sw_row_op(ks, 32 * sb, c, lane);
-      f32x16 s[2] = {};
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-#pragma unroll
-        for (int sb = 0; sb < 2; ++sb) s[sb] = mfma32(kop[sb][c], qreg[c], s[sb]);
-
-      // Partial tile: invisible pairs to -inf. With MASK16 (block size a
-      // multiple of 16) the mask is constant on 1-row x 16-key strips:
-      // registers 0-7 of a key block hold its keys 0-15, registers 8-15 keys
-      // 16-31, so one test per strip decides them.
-      if (cls == kPartial) {
-#pragma unroll
-        for (int sb = 0; sb < 2; ++sb) {
-          if (MASK16) {
-            const bool lo = iv_has(riv, k0 + 32 * sb), hi = iv_has(riv, k0 + 32 * sb + 16);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) s[sb][r] = (r < 8 ? lo : hi) ? s[sb][r] : -INFINITY;
-          } else {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int key = k0 + 32 * sb + 8 * (r >> 2) + 4 * g + (r & 3);
-              s[sb][r] = iv_has(riv, key) ? s[sb][r] : -INFINITY;
-            }
-          }
-        }
-      }
-      // Row max over the 32 scores: four independent v_max3 chains.
-      float mq[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        mq[q] = fmaxf(fmaxf(s[0][4 * q], s[0][4 * q + 1]), s[0][4 * q + 2]);
-        mq[q] = fmaxf(fmaxf(mq[q], s[0][4 * q + 3]), s[1][4 * q]);
-        mq[q] = fmaxf(fmaxf(mq[q], s[1][4 * q + 1]), s[1][4 * q + 2]);
-        mq[q] = fmaxf(mq[q], s[1][4 * q + 3]);
-      }
-      const float mx = fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]));
-      const float mt = max_xor32(mx) * a.scale_log2;
-      if (__ballot(mt > m + kRescale) != 0) {
-        const float mn = fmaxf(m, mt);
-        const float alpha = (mn == -INFINITY) ? 1.f : fast_exp2(m - mn);
-        m = mn;
-        lsum *= alpha;
-        o[0] *= alpha;
-        o[1] *= alpha;
-      }
-      const float mu = (m == -INFINITY) ? 0.f : m;
-      bf16x8 pop[2][2];  // P^T operands [key block][16-key step]
-#pragma unroll
-      for (int sb = 0; sb < 2; ++sb) {
-        float p[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) p[r] = fast_exp2(fmaf(s[sb][r], a.scale_log2, -mu));
-#pragma unroll
-        for (int kc = 0; kc < 2; ++kc) {
-          pop[sb][kc] = to_bf16x8(p[8 * kc], p[8 * kc + 1], p[8 * kc + 2], p[8 * kc + 3], p[8 * kc + 4],
-                                  p[8 * kc + 5], p[8 * kc + 6], p[8 * kc + 7]);
-          lsum = sum_bf16x8(pop[sb][kc], lsum);
-        }
-      }
-#pragma unroll
-      for (int sb = 0; sb < 2; ++sb) {
-        bf16x8 vop[2][2];  // V^T operands of key block sb [16-key step][d block], read just before use
-#pragma unroll
-        for (int kc = 0; kc < 2; ++kc)
-#pragma unroll
-          for (int db = 0; db < 2; ++db) vop[kc][db] = sw_tr_op(vs, 32 * sb + 16 * kc, 32 * db, lane);
-#pragma unroll
-        for (int kc = 0; kc < 2; ++kc)
-#pragma unroll
-          for (int db = 0; db < 2; ++db) o[db] = mfma32(vop[kc][db], pop[sb][kc], o[db]);
-      }
-    }
+    // Classes of the two 32-key halves for this wave's rows; a tile is
+    // partial when either live half is.
+    const int c0 = bounds_class(cb, k0, 32, a.n);
+    const int c1 = bounds_class(cb, k0 + 32, 32, a.n);
+#if BD3_FWD_HALF
+    const int cls = (c0 == kPartial || c1 == kPartial) ? kPartial : kFull;
+    if (c0 != kNone && c1 != kNone)
+      step(std::integral_constant<int, 2>(), 0, k0, cls, smem[cur][0], smem[cur][1]);
+    else if ((c0 | c1) != kNone)
+      step(std::integral_constant<int, 1>(), c0 != kNone ? 0 : 1, k0, cls, smem[cur][0], smem[cur][1]);
+#else
+    const int cls = (c0 == kFull && c1 == kFull) ? kFull : kPartial;
+    if ((c0 | c1) != kNone)
+      step(std::integral_constant<int, 2>(), 0, k0, cls, smem[cur][0], smem[cur][1]);
+#endif
     // Tile it+1 complete (the loads of later tiles may stay in flight), and
     // every wave is done reading stage `cur` before it is refilled.
     if (pf)
@@ -238,7 +278,7 @@ __global__ __launch_bounds__(256, OCC) void attn_fwd_dma_kernel(FwdArgs a) {
       *reinterpret_cast<bf16x4*>(op + 32 * db + 8 * rg4 + 4 * g) =
           to_bf16x4(o[db][4 * rg4] * inv, o[db][4 * rg4 + 1] * inv, o[db][4 * rg4 + 2] * inv,
                     o[db][4 * rg4 + 3] * inv);
-  if (g == 0) a.lse[(int64_t)bo.bh * 2 * a.n + myq] = (m + fast_log2(ltot)) * kLn2;
+  if (g == 0) a.lse[(int64_t)bo.bh * 2 * a.n + myq] = (mref + fast_log2(ltot)) * kLn2;
 }
 
 }  // namespace

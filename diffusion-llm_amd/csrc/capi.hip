@@ -46,6 +46,19 @@ int check_tensor(const void* p, const int64_t* st, const char* name) {
 
 bd3::Strides3 s3(const int64_t* st) { return bd3::Strides3{st[0], st[1], st[2]}; }
 
+// The training kernels fill LDS tiles of 64 rows with direct loads whose
+// per-lane byte offset from the tile's first row, 2 * (row * seq_stride +
+// column), is a 32-bit value: row <= 63 and column < 64 keep it below 2^31
+// for sequence strides below 2^24 elements.
+constexpr int64_t kMaxDmaSeqStride = int64_t(1) << 24;
+
+int check_dma_stride(const int64_t* st, const char* name) {
+  if (st[2] >= kMaxDmaSeqStride)
+    return fail(BD3_EINVAL, "%s sequence stride %lld must be < 2^24 elements (32-bit tile load offsets)", name,
+                (long long)st[2]);
+  return BD3_OK;
+}
+
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 constexpr int kDecodeQT = 32;
@@ -185,6 +198,10 @@ int bd3_attn_fwd(const void* q, const void* k, const void* v, void* o, float* ls
     int st = check_tensor(ptrs[i], strides + 3 * i, names[i]);
     if (st) return st;
   }
+  for (int i = 1; i < 3; ++i) {
+    int st = check_dma_stride(strides + 3 * i, names[i]);
+    if (st) return st;
+  }
   if (lse == nullptr) return fail(BD3_EINVAL, "lse is NULL");
   bd3::FwdArgs a;
   a.q = static_cast<const uint16_t*>(q);
@@ -219,6 +236,8 @@ int bd3_attn_bwd_dq(const void* q, const void* k, const void* v, const void* o, 
   const void* ptrs[6] = {q, k, v, o, dout, dq};
   for (int i = 0; i < 6; ++i)
     if ((st = check_tensor(ptrs[i], strides + 3 * i, names[i]))) return st;
+  for (int i = 1; i < 3; ++i)
+    if ((st = check_dma_stride(strides + 3 * i, names[i]))) return st;
   if (lse == nullptr || delta == nullptr) return fail(BD3_EINVAL, "lse and delta must be non-NULL");
   bd3::BwdArgs a = bwd_args(q, k, v, o, dout, lse, dq, nullptr, nullptr, delta, batch, heads, n,
                             block_size, scale);
@@ -241,6 +260,8 @@ int bd3_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* d
   const void* ptrs[6] = {q, k, v, dout, dk, dv};
   for (int i = 0; i < 6; ++i)
     if ((st = check_tensor(ptrs[i], strides + 3 * i, names[i]))) return st;
+  for (int i : {0, 3})
+    if ((st = check_dma_stride(strides + 3 * i, names[i]))) return st;
   if (lse == nullptr || delta == nullptr) return fail(BD3_EINVAL, "lse and delta must be non-NULL");
   bd3::BwdArgs a = bwd_args(q, k, v, nullptr, dout, lse, nullptr, dk, dv, const_cast<float*>(delta),
                             batch, heads, n, block_size, scale);
@@ -565,33 +586,52 @@ int bd3_train_tile_census(int32_t n, int32_t block_size, int64_t* out) {
   if (out == nullptr) return fail(BD3_EINVAL, "out is NULL");
   if (n < 128 || n % 128 != 0 || block_size < 1)
     return fail(BD3_EINVAL, "need n a positive multiple of 128 and block_size >= 1");
-  int64_t useful = 0, executed = 0, full = 0, partial = 0, skipped = 0;
+  int64_t useful = 0, full = 0, partial = 0, skipped = 0, exec_rows = 0, exec_keys = 0;
   for (int q = 0; q < 2 * n; ++q) useful += bd3::train_row_keys(q, n, block_size);
-  // The forward's schedule: 128-row workgroups visit the 64-key tiles of
-  // train_key_ranges; each 32-row wave classifies each 32-key sub-block.
+  // Query-stationary schedule (forward and dQ kernels): 128-row workgroups
+  // visit the 64-key tiles of train_key_ranges; each 32-row wave computes
+  // both 32-key halves of a tile when either holds a live pair for its rows.
   for (int q0 = 0; q0 < 2 * n; q0 += 128) {
     const bd3::KeyRanges kr = bd3::train_key_ranges(q0, 128, n, block_size, 64);
     const int ranges[2][2] = {{kr.t0, kr.t1}, {kr.t2, kr.t3}};
     for (int rg = 0; rg < 2; ++rg)
       for (int t = ranges[rg][0]; t < ranges[rg][1]; ++t)
-        for (int w = 0; w < 4; ++w)
+        for (int w = 0; w < 4; ++w) {
+          bool live = false;
           for (int sb = 0; sb < 2; ++sb) {
             const int c = bd3::train_class(q0 + 32 * w, 32, 64 * t + 32 * sb, 32, n, block_size);
-            if (c == bd3::kNone) {
-              ++skipped;
-            } else {
-              executed += 32 * 32;
-              if (c == bd3::kFull) ++full; else ++partial;
-            }
+            if (c == bd3::kNone) ++skipped;
+            else if (c == bd3::kFull) ++full;
+            else ++partial;
+            live = live || c != bd3::kNone;
           }
+          if (live) exec_rows += 32 * 64;
+        }
+  }
+  // Key-stationary schedule (dK/dV kernel): 128-key workgroups visit the
+  // 64-row tiles of train_query_ranges; each 32-key wave computes both 32-row
+  // halves of a tile when either holds a live pair for its keys.
+  for (int k0 = 0; k0 < 2 * n; k0 += 128) {
+    const bd3::KeyRanges qr = bd3::train_query_ranges(k0, 128, n, block_size, 64);
+    const int ranges[2][2] = {{qr.t0, qr.t1}, {qr.t2, qr.t3}};
+    for (int rg = 0; rg < 2; ++rg)
+      for (int t = ranges[rg][0]; t < ranges[rg][1]; ++t)
+        for (int w = 0; w < 4; ++w) {
+          const bd3::KeyGroup g = bd3::train_key_group(k0 + 32 * w, 32, n, block_size);
+          if (bd3::key_group_class(g, 64 * t, 32, n) != bd3::kNone ||
+              bd3::key_group_class(g, 64 * t + 32, 32, n) != bd3::kNone)
+            exec_keys += 32 * 64;
+        }
   }
   const int64_t nn = n, bs = block_size;
   out[0] = useful;
-  out[1] = executed;
+  out[1] = exec_rows;
   out[2] = full;
   out[3] = partial;
   out[4] = skipped;
   out[5] = nn * nn + nn * bs;
+  out[6] = exec_rows;
+  out[7] = exec_keys;
   return BD3_OK;
 }
 

@@ -328,13 +328,18 @@ int bd3_mask_dump(uint8_t* out, int32_t mode, int32_t rows, int32_t kv_len,
 
 /*
  * Host-only (no GPU needed): tile census of the training-attention
- * schedule. Writes out[0..5] =
- *   {useful pairs, executed pairs (32x32 sub-blocks the forward computes),
- *    full sub-blocks, partial sub-blocks, skipped sub-blocks,
- *    useful pairs per (b,h) closed form n^2 + n*bs}
- * for one (batch, head). Mirrors the reference's tile-skipping ranges
- * (kernels/BlockSparseFlashAttention.py:132-164) at the library's own
- * sub-block granularity.
+ * schedules for one (batch, head). Writes out[0..7] =
+ *   {useful pairs,
+ *    pairs the forward kernel computes (its 32-row waves compute both 32-key
+ *      halves of a 64-key tile when either half has a live pair),
+ *    full / partial / skipped 32x32 sub-blocks of that schedule,
+ *    useful pairs per (b,h) closed form n^2 + n*bs,
+ *    pairs the dQ kernel computes (the forward's schedule),
+ *    pairs the dK/dV kernel computes (32-key waves, both 32-row halves of a
+ *      64-row tile when either has a live pair)}.
+ * `out` must hold 8 values. Mirrors the reference's tile-skipping ranges
+ * (kernels/BlockSparseFlashAttention.py:132-164, :274-325, :419-450) at the
+ * library's own tile granularity.
  */
 int bd3_train_tile_census(int32_t n, int32_t block_size, int64_t* out);
 

@@ -44,14 +44,19 @@ def test_abi_version(lib):
 @pytest.mark.parametrize("n,bs", [(128, 1), (128, 16), (256, 4), (256, 100), (384, 64), (512, 512),
                                   (1024, 16), (2048, 256)])
 def test_census_matches_oracle(lib, n, bs):
-    out = (ctypes.c_int64 * 6)()
+    out = (ctypes.c_int64 * 8)()
     assert lib.bd3_train_tile_census(n, bs, out) == 0
     m = block_diff_mask(n, bs)
     assert out[0] == int(m.sum())            # useful pairs
     if n % bs == 0:
         assert out[5] == out[0] == n * n + n * bs
-    assert out[1] >= out[0]                  # executed covers useful
-    assert out[1] == 1024 * (out[2] + out[3])
+    # executed pairs of each schedule recounted from the mask at its granularity:
+    # (32 rows x 64 keys) for the forward / dQ, (64 rows x 32 keys) for dK/dV
+    rows = m.reshape(2 * n // 32, 32, 2 * n // 64, 64).any(axis=(1, 3))
+    keys = m.reshape(2 * n // 64, 64, 2 * n // 32, 32).any(axis=(1, 3))
+    assert out[1] == out[6] == 2048 * int(rows.sum())
+    assert out[7] == 2048 * int(keys.sum())
+    assert out[1] >= 1024 * (out[2] + out[3]) >= out[0]
 
 
 @pytest.mark.parametrize("n,bs", [(64, 1), (64, 16), (96, 7), (128, 32), (128, 128), (160, 64),
@@ -128,6 +133,32 @@ def test_bwd_validation(lib):
     expect_einval(lib.bd3_attn_bwd_dkdv(*[GOOD] * 8, 1, 1, 128, 64, 5, st18, 0.125, None), "block_size")
     expect_einval(lib.bd3_attn_bwd_dkdv(GOOD, GOOD, GOOD, GOOD + 8, *[GOOD] * 4, 1, 1, 128, 64, 16, st18,
                                         0.125, None), "dout")
+
+
+def test_tile_load_offset_stride_limit(lib):
+    """Sequence strides of the tensors the training kernels load tile by tile
+    (k, v in the forward and dQ kernels; q, dO in dK/dV) must keep the 32-bit
+    per-lane load offsets in range: < 2^24 elements."""
+    big = 1 << 24
+    ok = [64 * 256, 64 * 256, 64]
+    for slot, name in ((1, "k"), (2, "v")):
+        st = [*ok * 4]
+        st[3 * slot + 2] = big
+        expect_einval(lib.bd3_attn_fwd(GOOD, GOOD, GOOD, GOOD, GOOD, 1, 1, 128, 64, 16, _i64(st), 0.125, None),
+                      f"{name} sequence stride")
+        st18 = [*ok * 6]
+        st18[3 * slot + 2] = big
+        expect_einval(lib.bd3_attn_bwd_dq(*[GOOD] * 8, 1, 1, 128, 64, 16, _i64(st18), 0.125, None),
+                      f"{name} sequence stride")
+    for slot, name in ((0, "q"), (3, "dout")):
+        st18 = [*ok * 6]
+        st18[3 * slot + 2] = big
+        expect_einval(lib.bd3_attn_bwd_dkdv(*[GOOD] * 8, 1, 1, 128, 64, 16, _i64(st18), 0.125, None),
+                      f"{name} sequence stride")
+    # q's stride in the forward is not a tile-load offset: only the 8-alignment applies
+    st = [big - 8, 64, 64] + ok * 3
+    status = lib.bd3_attn_fwd(GOOD, GOOD, GOOD, GOOD, None, 1, 1, 128, 64, 16, _i64(st), 0.125, None)
+    expect_einval(status, "lse")  # passed the stride checks, stopped at the next one
 
 
 def test_decode_validation(lib):
