@@ -95,6 +95,43 @@ def bd3_attention_grads(q: Tensor, k: Tensor, v: Tensor, dout: Tensor, block_siz
     return tuple(torch.cat([p[j] for p in parts]).reshape(B, H, S, D) for j in range(4))
 
 
+def bd3_attention_grads_rows(q: Tensor, k: Tensor, v: Tensor, dout: Tensor, block_size: int,
+                             rows: int = 1024) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """(O, lse, dQ, dK, dV) of one (b, h) slice (tensors (S, d), fp32), the
+    same values as bd3_attention / bd3_attention_grads with memory bounded to
+    `rows` x S scores at a time: for long sequences (2n = 8192, 16384), where
+    the dense autograd graph holds several S x S fp32 intermediates.
+
+    Written out from the eager path's closed-form gradients (the reference
+    differentiates model/modules.py:738-771 with autograd): per row block,
+    P = softmax(S * scale + M) (M from model/bd3lm.py:10-52), O = P V cast as
+    the reference casts P to v's dtype, Delta = rowsum(dO o O),
+    dP = dO V^T, dS = P o (dP - Delta), dQ = scale dS K; dK += scale dS^T Q and
+    dV += P^T dO summed over the row blocks."""
+    S, D = q.shape
+    n = S // 2
+    scale = 1.0 / D ** 0.5
+    mask = train_mask(n, block_size)
+    o = torch.empty_like(q)
+    lse = torch.empty(S, dtype=q.dtype)
+    dq = torch.empty_like(q)
+    dk = torch.zeros_like(k)
+    dv = torch.zeros_like(v)
+    for r0 in range(0, S, rows):
+        sl = slice(r0, min(r0 + rows, S))
+        s = torch.matmul(q[sl], k.transpose(-1, -2)) * scale
+        s = torch.where(mask[sl], s, -torch.inf)
+        lse[sl] = torch.logsumexp(s, dim=-1)
+        p = softmax(s, dim=-1)
+        o[sl] = torch.matmul(p.to(v.dtype), v)
+        delta = (dout[sl] * o[sl]).sum(-1, keepdim=True)
+        ds = p * (torch.matmul(dout[sl], v.transpose(-1, -2)) - delta)
+        dq[sl] = torch.matmul(ds, k) * scale
+        dk += torch.matmul(ds.transpose(-1, -2), q[sl]) * scale
+        dv += torch.matmul(p.transpose(-1, -2), dout[sl])
+    return o, lse, dq, dk, dv
+
+
 def decode_attention(q: Tensor, k: Tensor, v: Tensor, block_size: int,
                      logits_dtype: torch.dtype = torch.float32) -> Tensor:
     """Block-causal attention of the last q_len positions over kv_len keys

@@ -8,8 +8,8 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from oracle.attention import (bd3_attention, bd3_attention_grads, decode_attention,
-                              eager_attention, masked_lse, split_merge, split_partials,
+from oracle.attention import (bd3_attention, bd3_attention_grads, bd3_attention_grads_rows,
+                              decode_attention, eager_attention, masked_lse, split_merge, split_partials,
                               train_mask, useful_flops_fwd)
 
 GOLDEN = json.loads((Path(__file__).parent / "golden" / "bd3_golden.json").read_text())
@@ -103,6 +103,21 @@ def test_chunked_equals_unchunked():
     a = bd3_attention_grads(q, k, v, do, bs, logits_dtype=torch.float64)
     b = bd3_attention_grads(q, k, v, do, bs, chunk=4, logits_dtype=torch.float64)
     assert all(torch.allclose(x, y, atol=1e-12) for x, y in zip(a, b))
+
+
+@pytest.mark.parametrize("n,bs,rows", [(64, 4, 16), (64, 16, 48), (128, 32, 128), (96, 1, 40)])
+def test_row_blocked_grads_equal_autograd(n, bs, rows):
+    """The row-blocked closed-form oracle (long sequences) gives the dense
+    autograd values, in float64, whatever the row block (including blocks
+    that straddle the noisy / clean halves and a ragged last block)."""
+    d = 16
+    q, k, v, do = (rand(1, 1, 2 * n, d, seed=s + 70)[0, 0].double() for s in range(4))
+    o, lse, dq, dk, dv = bd3_attention_grads_rows(q, k, v, do, bs, rows=rows)
+    ro, rdq, rdk, rdv = bd3_attention_grads(q[None, None], k[None, None], v[None, None], do[None, None], bs,
+                                            logits_dtype=torch.float64)
+    _, rlse = bd3_attention(q[None, None], k[None, None], v[None, None], bs, logits_dtype=torch.float64)
+    for got, ref in ((o, ro), (lse, rlse), (dq, rdq), (dk, rdk), (dv, rdv)):
+        assert torch.allclose(got.double(), ref[0, 0].double(), rtol=1e-10, atol=1e-10)
 
 
 def test_cached_decode_step_is_unmasked_sdpa():
