@@ -1,15 +1,23 @@
 """Attention-backend registry: the operator seam of the BD3-LM model.
 
-Mirrors the reference's bench/attention.py:51-127. A model module exposes a
-global `scaled_dot_product_attention(q, k, v, mask=None)` that its attention
-layer looks up by name at call time (model/modules.py:419);
-`install_attention(name, block_size=...)` replaces that global with one of
-the gfx950 backends below. The block-size backends ignore `mask` and rebuild
-the BD3-LM mask from `block_size`, exactly as the reference's do (:51-66):
+The reference model's attention layer calls a module-level function
+`scaled_dot_product_attention(q, k, v, mask=None)` that it resolves by name
+at call time (model/modules.py:419), and the reference swaps that function
+with `install_attention(name, nvtx, block_size)` (bench/attention.py:117-127).
+This module keeps that public surface (the `BACKENDS` names, the
+`BLOCK_SIZE_BACKENDS` tuple and `install_attention`'s signature) so a caller
+switches over by name, and routes each name to the gfx950 library through the
+`torch.ops.bd3` custom ops (kernels/ops.py), which trace under torch.compile
+without a graph break.
 
-    bsfa      training layout cat(x_t, x_0), forward + backward
-    bsdfa     decode / prefill: last q_len positions, block-causal
-    split_kv  bsdfa with the keys split across workgroups
+Backends taking a block size do not read `mask`: each one derives the
+visibility rule from the block size and the layout it serves.
+
+    name      layout of (q, k, v)                         rule
+    bsfa      training sequence cat(x_t, x_0), length 2n  BD3-LM mask; fwd + bwd
+    bsdfa     q = last q_len of the kv_len positions      block-causal; fwd only
+    split_kv  as bsdfa                                    as bsdfa, keys cut into
+                                                          the reference's 256-key splits
 """
 from __future__ import annotations
 
@@ -25,31 +33,32 @@ import kernels.ops  # noqa: F401  (registers torch.ops.bd3.*)
 
 AttentionFn = Callable[..., Tensor]
 
+# Profiler range names (roctx on ROCm builds), as the reference names them.
 FORWARD_RANGE = "attention"
 BACKWARD_RANGE = "attention backward"
 
-
-# The backends call the custom ops (kernels/ops.py), so a caller wrapped in
-# torch.compile traces them without a graph break.
+# split count argument of torch.ops.bd3.decode: 0 = the library's automatic
+# count, -1 = the reference's ceil(kv_len / 256) rule
+_AUTO_SPLITS, _REFERENCE_SPLITS = 0, -1
 
 
 def bsfa(q, k, v, mask=None, block_size=None):
-    """Block-sparse FlashAttention (forward + backward) on the 2n training
-    layout; it builds the mask from block_size."""
+    """Training attention over cat(x_t, x_0) under the BD3-LM mask of
+    `block_size`; differentiable (bd3_attn_fwd / bd3_attn_bwd)."""
     return torch.ops.bd3.attn_fwd(q, k, v, block_size)[0]
 
 
 def bsdfa(q, k, v, mask=None, block_size=None):
-    """Block-sparse decode attention (forward only): the last q_len
-    positions, block-causal; it builds the mask from block_size."""
-    return torch.ops.bd3.decode(q, k, v, block_size, 0)
+    """Decode / prefill attention: q holds the last q_len of the kv_len key
+    positions, visibility block-causal in `block_size` (bd3_decode, automatic
+    split count)."""
+    return torch.ops.bd3.decode(q, k, v, block_size, _AUTO_SPLITS)
 
 
 def split_kv(q, k, v, mask=None, block_size=None):
-    """Split-KV decode attention (forward only): bsdfa with the keys split
-    across workgroups, for decode steps with few queries (the reference's
-    split rule)."""
-    return torch.ops.bd3.decode(q, k, v, block_size, -1)
+    """Same result as bsdfa, with the keys cut into ceil(kv_len / 256) splits
+    merged by their log-sum-exp (bd3_decode_splitkv)."""
+    return torch.ops.bd3.decode(q, k, v, block_size, _REFERENCE_SPLITS)
 
 
 BACKENDS: dict[str, AttentionFn] = {
@@ -57,47 +66,47 @@ BACKENDS: dict[str, AttentionFn] = {
     "bsdfa": bsdfa,
     "split_kv": split_kv,
 }
-# backends that ignore the mask and need the block size instead
 BLOCK_SIZE_BACKENDS = ("bsfa", "bsdfa", "split_kv")
 
 
-class _OpenRange(torch.autograd.Function):
-    """Identity on (q, k, v) that opens the forward range (roctx on ROCm)."""
+class _RangeEdge(torch.autograd.Function):
+    """Passes its tensors through unchanged and marks one edge of the
+    attention's profiler ranges on the way.
+
+    Placed at the attention's inputs (`entry=True`) it opens the forward
+    range and, when the gradients come back through it, closes the backward
+    range; placed at the output it closes the forward range and opens the
+    backward one. Autograd runs the two backward edges in the reverse order
+    of the forward ones, so the ranges nest."""
 
     @staticmethod
-    def forward(ctx, q, k, v):
-        torch.cuda.nvtx.range_push(FORWARD_RANGE)
-        return q.view_as(q), k.view_as(k), v.view_as(v)
+    def forward(ctx, entry: bool, *xs: Tensor):
+        ctx.entry = entry
+        if entry:
+            torch.cuda.nvtx.range_push(FORWARD_RANGE)
+        else:
+            torch.cuda.nvtx.range_pop()
+        return tuple(x.view_as(x) for x in xs)
 
     @staticmethod
-    def backward(ctx, *grad_outputs):
-        torch.cuda.nvtx.range_pop()
-        return grad_outputs
-
-
-class _CloseRange(torch.autograd.Function):
-    """Identity on the attention output that closes the forward range."""
-
-    @staticmethod
-    def forward(ctx, o):
-        torch.cuda.nvtx.range_pop()
-        return o.view_as(o)
-
-    @staticmethod
-    def backward(ctx, *grad_outputs):
-        torch.cuda.nvtx.range_push(BACKWARD_RANGE)
-        return grad_outputs
+    def backward(ctx, *grads: Tensor):
+        if ctx.entry:
+            torch.cuda.nvtx.range_pop()
+        else:
+            torch.cuda.nvtx.range_push(BACKWARD_RANGE)
+        return (None, *grads)
 
 
 def with_ranges(attention: AttentionFn) -> AttentionFn:
-    """Wrap a backend in profiler ranges for both forward and backward
-    (reference: with_nvtx, bench/attention.py:107-114)."""
+    """`attention` with its forward and backward each inside a profiler range
+    (the reference's nvtx=True option, bench/attention.py:107-114)."""
 
-    def annotated(q, k, v, mask=None):
-        q, k, v = _OpenRange.apply(q, k, v)
-        return _CloseRange.apply(attention(q, k, v, mask))
+    def ranged(q, k, v, mask=None):
+        q, k, v = _RangeEdge.apply(True, q, k, v)
+        (o,) = _RangeEdge.apply(False, attention(q, k, v, mask))
+        return o
 
-    return annotated
+    return ranged
 
 
 def install_attention(
@@ -106,19 +115,19 @@ def install_attention(
     block_size: int | None = None,
     module: ModuleType | str = "model.modules",
 ) -> AttentionFn:
-    """Route every attention layer of `module` through the named backend
-    (reference: bench/attention.py:117-127). `module` is the model module
-    whose global `scaled_dot_product_attention` the attention layer calls;
-    names not registered here (e.g. the model's own eager "custom") are
-    looked up on that module. Returns the installed callable."""
+    """Make `module.scaled_dot_product_attention` the backend `name` and
+    return what was installed (reference: bench/attention.py:117-127).
+
+    `module` is the model module whose attention layer looks the function up
+    (the reference patches its own `model.modules`). A name this registry does
+    not hold (e.g. the model's eager "custom") is taken from that module's
+    own `BACKENDS`. Block-size backends need `block_size`."""
     mod = importlib.import_module(module) if isinstance(module, str) else module
-    if name in BACKENDS:
-        attention = BACKENDS[name]
-    else:
-        attention = getattr(mod, "BACKENDS", {})[name]
+    attention = BACKENDS.get(name) or getattr(mod, "BACKENDS", {})[name]
     if name in BLOCK_SIZE_BACKENDS:
         assert block_size is not None, f"{name} needs block_size"
         attention = partial(attention, block_size=block_size)
-    installed = with_ranges(attention) if nvtx else attention
-    mod.scaled_dot_product_attention = installed
-    return installed
+    if nvtx:
+        attention = with_ranges(attention)
+    mod.scaled_dot_product_attention = attention
+    return attention

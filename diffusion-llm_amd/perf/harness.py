@@ -1,118 +1,119 @@
-"""Benchmark + correctness harness: bench, check, log_result.
+"""Device timing for the benchmarks: per-call HIP-event samples taken on the
+launch stream, each call preceded by an eviction of the GPU caches.
 
-Mirrors the reference's bench/harness.py:25-91 with two MI355X changes:
-  * the cache flush between timed reps reads 1 GiB (the reference zeroes
-    256 MiB, :32-33, which does not clear MI355X's 256 MB Infinity Cache on
-    top of the 4 MB-per-XCD L2, and a zeroing pass would leave dirty lines
-    whose write-back competes with the timed kernel);
-  * timestamps are UTC via timezone.utc (Python 3.10 has no datetime.UTC).
+The reference times its kernels with CUDA events after clearing a 256 MiB
+buffer (bench/harness.py:25-51). On MI355X that does not empty the caches a
+kernel's inputs may sit in: 4 MB of L2 per XCD plus the 256 MB Infinity
+Cache in front of HBM. `CacheEvictor` therefore streams a 1 GiB buffer
+through them with a read (a reduction), which leaves clean lines behind; a
+zeroing pass would leave dirty lines whose write-back would then compete
+with the timed call for HBM.
+
+    samples = time_calls(fn, reps=30, warmup=5)   # flush, event, fn(), event
+    samples.median_ms, samples.quantile_ms(0.2), samples.mean_ms
 """
 from __future__ import annotations
 
-import json
-import os
+import statistics
 import time
-from collections.abc import Callable
-from dataclasses import asdict, dataclass
-from datetime import datetime, timezone
-from pathlib import Path
+from collections.abc import Callable, Sequence
 from typing import Any
 
 import torch
-from torch import Tensor
 
-RESULTS_DIR = Path(os.environ.get("RESULTS_DIR", "results"))
-FLUSH_BYTES = 1 << 30
+EVICT_BYTES = 1 << 30
 
 
-@dataclass
-class Timing:
-    median_ms: float
-    p20_ms: float
-    p80_ms: float
-    mean_ms: float
-    n_iters: int
+class CacheEvictor:
+    """Owns the eviction buffer (allocated on first use, on the current
+    device) and reads it through the caches on `evict()`."""
+
+    def __init__(self, nbytes: int = EVICT_BYTES):
+        self.nbytes = nbytes
+        self._buf: torch.Tensor | None = None
+
+    def evict(self) -> None:
+        if self._buf is None:
+            self._buf = torch.ones(self.nbytes // 4, dtype=torch.int32, device="cuda")
+        self._buf.max()
 
 
-_flush_buf: Tensor | None = None
+_EVICTOR = CacheEvictor()
 
 
 def flush_caches() -> None:
-    """Evict L2 and the Infinity Cache by reading a 1 GiB buffer. A read
-    leaves the caches holding clean lines; zeroing the buffer (the
-    reference's method) would leave up to the cache capacity of dirty lines
-    whose write-back then competes with the timed kernel for HBM."""
-    global _flush_buf
-    if _flush_buf is None:
-        _flush_buf = torch.zeros(FLUSH_BYTES // 4, dtype=torch.int32, device="cuda")
-    _flush_buf.max()
+    """Evict L2 and the Infinity Cache with the shared 1 GiB read."""
+    _EVICTOR.evict()
 
 
-def bench(fn: Callable[[], Any], warmup: int = 25, rep: int = 100, flush: bool = True) -> Timing:
-    """Time fn() over `rep` calls after `warmup` untimed ones; HIP events on
-    the current stream bracket each call (reference bench(), :25-51)."""
+class Samples:
+    """Per-call durations in milliseconds, with the summary statistics the
+    bench records report."""
+
+    def __init__(self, ms: Sequence[float]):
+        if not ms:
+            raise ValueError("no samples")
+        self.ms = sorted(float(x) for x in ms)
+
+    def quantile_ms(self, p: float) -> float:
+        """Linear-interpolated quantile, 0 <= p <= 1."""
+        pos = p * (len(self.ms) - 1)
+        lo = int(pos)
+        hi = min(lo + 1, len(self.ms) - 1)
+        return self.ms[lo] + (self.ms[hi] - self.ms[lo]) * (pos - lo)
+
+    @property
+    def median_ms(self) -> float:
+        return self.quantile_ms(0.5)
+
+    @property
+    def p20_ms(self) -> float:
+        return self.quantile_ms(0.2)
+
+    @property
+    def p80_ms(self) -> float:
+        return self.quantile_ms(0.8)
+
+    @property
+    def mean_ms(self) -> float:
+        return statistics.fmean(self.ms)
+
+    @property
+    def n_iters(self) -> int:
+        return len(self.ms)
+
+
+def time_calls(fn: Callable[[], Any], reps: int = 30, warmup: int = 5, flush: bool = True,
+               stream: torch.cuda.Stream | None = None) -> Samples:
+    """Run fn() `warmup` times untimed, then `reps` times, each timed by a
+    pair of HIP events recorded on `stream` (default: the current stream,
+    which is where the library's wrappers launch). With `flush`, the caches
+    are evicted before every timed call, outside the events. Without a GPU
+    the host clock times each call instead."""
     for _ in range(warmup):
         fn()
-    if torch.cuda.is_available():
-        torch.cuda.synchronize()
-        events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                  for _ in range(rep)]
-        for start, end in events:
-            if flush:
-                flush_caches()
-            start.record()
-            fn()
-            end.record()
-        torch.cuda.synchronize()
-        times = [s.elapsed_time(e) for s, e in events]
-    else:
-        times = []
-        for _ in range(rep):
+    if not torch.cuda.is_available():
+        ms = []
+        for _ in range(reps):
             t0 = time.perf_counter()
             fn()
-            times.append((time.perf_counter() - t0) * 1e3)
-    t = torch.tensor(times, dtype=torch.float64)
-    p20, p50, p80 = torch.quantile(t, torch.tensor([0.2, 0.5, 0.8], dtype=torch.float64)).tolist()
-    return Timing(median_ms=p50, p20_ms=p20, p80_ms=p80, mean_ms=float(t.mean()), n_iters=rep)
+            ms.append((time.perf_counter() - t0) * 1e3)
+        return Samples(ms)
+    stream = stream or torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    marks = []
+    for _ in range(reps):
+        if flush:
+            flush_caches()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        fn()
+        stop.record(stream)
+        marks.append((start, stop))
+    torch.cuda.synchronize()
+    return Samples([a.elapsed_time(b) for a, b in marks])
 
 
-@dataclass
-class Check:
-    passed: bool
-    max_abs: float
-    max_rel: float
-    cosine: float
-
-
-def check(out: Tensor, ref: Tensor, atol: float = 1e-5, rtol: float = 1e-4) -> Check:
-    """Compare in float64; pass iff every |out - ref| <= atol + rtol * |ref|
-    (a NaN fails) (reference check(), :62-72)."""
-    o = out.detach().double().flatten().cpu()
-    r = ref.detach().double().flatten().cpu()
-    diff = (o - r).abs()
-    return Check(
-        passed=bool((diff <= atol + rtol * r.abs()).all()),
-        max_abs=diff.max().item(),
-        max_rel=(diff / r.abs().clamp_min(1e-12)).max().item(),
-        cosine=torch.nn.functional.cosine_similarity(o, r, dim=0).item(),
-    )
-
-
-def log_result(name: str, config: dict, timing: Timing | None = None,
-               check: Check | None = None, **metrics: Any) -> None:
-    """Append one run (config, timing, check, environment) to
-    RESULTS_DIR/<name>.jsonl (reference log_result(), :75-91)."""
-    record = {
-        "time": datetime.now(timezone.utc).isoformat(timespec="seconds"),
-        "config": config,
-        "timing": asdict(timing) if timing else None,
-        "check": asdict(check) if check else None,
-        "env": {
-            "gpu": torch.cuda.get_device_name() if torch.cuda.is_available() else "cpu",
-            "torch": torch.__version__,
-        },
-        **metrics,
-    }
-    RESULTS_DIR.mkdir(parents=True, exist_ok=True)
-    with (RESULTS_DIR / f"{name}.jsonl").open("a") as f:
-        f.write(json.dumps(record, default=str) + "\n")
+def bench(fn: Callable[[], Any], warmup: int = 5, rep: int = 30, flush: bool = True) -> Samples:
+    """time_calls with the argument names the bench sections use."""
+    return time_calls(fn, reps=rep, warmup=warmup, flush=flush)
