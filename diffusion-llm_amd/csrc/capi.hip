@@ -5,6 +5,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
 #include <string>
 
 #include "bd3_launch.h"
@@ -302,6 +303,68 @@ int bd3_attn_bwd(const void* q, const void* k, const void* v, const void* o, con
   if (st) return st;
   return bd3_attn_bwd_dkdv(q, k, v, dout, lse, delta, dk, dv, batch, heads, n, head_dim, block_size,
                            kv_strides, scale, stream);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Backward without a caller workspace (bd3_attn_bwd_noalloc): the Delta and
+// L * log2(e) planes live in `scratch`, a device array of this library that
+// each GPU holds from the library's first use on it until the process ends.
+// Host code never passes the array's name to a kernel (on the host it is a
+// stand-in, not a device address): the address each device gives
+// hipGetSymbolAddress is looked up once per device, with that device
+// current, and only that address is used.
+namespace {
+
+constexpr size_t kScratchBytes = 2 * sizeof(float) * BD3_NOALLOC_MAX_ROWS;  // 8 MiB: 2 planes
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch`, looked up on the device's first
+// call (the caller's current device is the device of `stream`, as for every
+// entry point).
+int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(BD3_EINVAL, "device %d beyond the scratch table", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_status(e, "hipGetSymbolAddress(scratch)");
+    if (ptr == nullptr) return fail(BD3_EHIP, "hipGetSymbolAddress(scratch) returned NULL");
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return BD3_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int bd3_attn_bwd_noalloc(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                         const float* lse, void* dq, void* dk, void* dv, int32_t batch, int32_t heads,
+                         int32_t n, int32_t head_dim, int32_t block_size, const int64_t* strides, float scale,
+                         void* stream) {
+  int st = check_bwd_shape(batch, heads, n, head_dim, block_size, strides);
+  if (st) return st;
+  const size_t need = bd3_attn_bwd_workspace_bytes(batch, heads, n, head_dim);
+  if (need > kScratchBytes)
+    return fail(BD3_EINVAL,
+                "bd3_attn_bwd_noalloc holds at most %d rows (batch * heads * 2n = %lld): use bd3_attn_bwd with a "
+                "workspace", BD3_NOALLOC_MAX_ROWS, (long long)batch * heads * 2 * n);
+  void* ws = nullptr;
+  if ((st = scratch_address(&ws))) return st;
+  // Every element of both planes is written by the dQ stage before the dK/dV
+  // stage reads it, so nothing needs clearing between calls.
+  return bd3_attn_bwd(q, k, v, o, dout, lse, dq, dk, dv, ws, kScratchBytes, batch, heads, n, head_dim,
+                      block_size, strides, scale, stream);
 }
 
 int32_t bd3_decode_auto_splits(int32_t batch, int32_t heads, int32_t q_len, int32_t kv_len) {

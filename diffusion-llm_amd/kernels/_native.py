@@ -34,6 +34,8 @@ SIGNATURES: dict[str, tuple] = {
     "bd3_attn_bwd_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32]),
     "bd3_attn_bwd": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _sz,
                                     _i32, _i32, _i32, _i32, _i32, _i64p, _f32, _c_p]),
+    "bd3_attn_bwd_noalloc": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _i32, _i32,
+                                            _i32, _i32, _i32, _i64p, _f32, _c_p]),
     "bd3_attn_bwd_dq": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _i32, _i32, _i32,
                                        _i32, _i32, _i64p, _f32, _c_p]),
     "bd3_attn_bwd_dkdv": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _i32, _i32, _i32,

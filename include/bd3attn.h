@@ -97,6 +97,28 @@ int bd3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
                  void* stream);
 
 /*
+ * bd3_attn_bwd without a workspace argument: the same kernels and results
+ * (bit for bit), with the Delta and L * log2(e) planes kept in a fixed
+ * device array inside the library (8 MiB per GPU, held from the library's
+ * first call of this function on that GPU until the process ends).
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops that forbid
+ * hipMalloc). Makes no allocation of any kind.
+ * Limit: batch * heads * 2n <= BD3_NOALLOC_MAX_ROWS (e.g. B=8, H=12,
+ * 2n=8192); larger calls return BD3_EINVAL. Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (different streams or
+ * threads, no ordering between them) race and must not be made. The calling
+ * thread's current device must be the device of `stream`.
+ */
+#define BD3_NOALLOC_MAX_ROWS (1 << 20)
+int bd3_attn_bwd_noalloc(const void* q, const void* k, const void* v,
+                         const void* o, const void* dout, const float* lse,
+                         void* dq, void* dk, void* dv, int32_t batch,
+                         int32_t heads, int32_t n, int32_t head_dim,
+                         int32_t block_size, const int64_t* strides,
+                         float scale, void* stream);
+
+/*
  * Backward, first stage: dQ = scale * dS K with dS = P o (dP - Delta),
  * and, for the second stage, Delta = rowsum(dO * O) and the forward's L
  * times log2(e) written to `delta`: fp32, contiguous (2, batch, heads, 2n),
