@@ -64,8 +64,14 @@ struct DecodeArgs {
   int kv_len;
   int bs;
   int n_splits;
-  int split_len;  // keys per split (multiple of 64)
+  int split_len;  // keys per split (multiple of 32)
   int q_tiles;
+  // Workgroups per (bh, query tile) along the splits, and the consecutive
+  // splits each one computes (groups * splits_per_group >= n_splits). With
+  // one split per group the workgroup's waves share the split; with more,
+  // each wave computes whole splits and the workgroup merges them.
+  int groups;
+  int splits_per_group;
   float scale_log2;
 };
 

@@ -167,11 +167,29 @@ int run_decode(const void* q, const void* k, const void* v, void* o, int32_t bat
   a.kv_len = kv_len;
   a.bs = block_size;
   a.n_splits = n_splits;
-  // Split length: ceil(kv_len / n_splits) rounded up to 16 keys.
+  // Split length: ceil(kv_len / n_splits) rounded up to whole 32-key chunks
+  // (the kernels' load and compute unit; a split ending mid-chunk would load
+  // the chunk's other half twice).
   int sl = (kv_len + n_splits - 1) / n_splits;
-  sl = (sl + 15) / 16 * 16;
+  sl = (sl + 31) / 32 * 32;
   a.split_len = sl;
   a.q_tiles = q_tiles;
+  // One workgroup per split, unless that overfills the GPU: then (cached
+  // steps, q_len <= 16) a workgroup computes several consecutive splits and
+  // merges their partials on chip, so that only enough workgroups for one
+  // per CU remain (at configs[3], 384 heads: every split count gives one
+  // workgroup per head, no partials in memory, no merge pass).
+  a.groups = n_splits;
+  a.splits_per_group = 1;
+  const int64_t units = (int64_t)batch * heads * q_tiles;
+  if (q_len <= 16 && n_splits >= 4 && units * n_splits > 512) {
+    const int64_t g = (256 + units - 1) / units;
+    const int per = (int)((n_splits + g - 1) / g);
+    if (per >= 4) {
+      a.splits_per_group = per;
+      a.groups = (n_splits + per - 1) / per;
+    }
+  }
   a.scale_log2 = scale * bd3::kLog2e;
   return hip_status(bd3::launch_decode(a, kDecodeQT, static_cast<hipStream_t>(stream)), "decode launch");
 }

@@ -190,9 +190,9 @@ __global__ __launch_bounds__(kThreads) void decode_partial(DecodeArgs a) {
   }
   __syncthreads();
 
-  const int split_out = a.n_splits > 1;
+  const int split_out = a.groups > 1;
   uint16_t* op = a.o + b * a.so.b + h * a.so.h;
-  const int64_t slot = ((int64_t)bh * a.q_tiles + qt) * a.n_splits + split;
+  const int64_t slot = ((int64_t)bh * a.q_tiles + qt) * a.groups + split;
 #pragma unroll
   for (int j = 0; j < (kQT * kHeadDim) / kThreads; ++j) {
     const int e = tid + kThreads * j;
@@ -270,7 +270,7 @@ __global__ __launch_bounds__(NW * 64, BD3_DEC16_OCC) void decode16_partial(Decod
   __bf16* ks = reinterpret_cast<__bf16*>(smem) + wave * 2 * kTile16;
   __bf16* vs = ks + kTile16;
 
-  const int split = blockIdx.x;
+  const int grp = blockIdx.x;
   const int bh = blockIdx.z;
   const int b = bh / a.heads, h = bh - b * a.heads;
   const uint16_t* qp = a.q + b * a.sq.b + h * a.sq.h;
@@ -287,28 +287,14 @@ __global__ __launch_bounds__(NW * 64, BD3_DEC16_OCC) void decode16_partial(Decod
   const int khi = l16 < a.q_len ? imin((pos / a.bs + 1) * a.bs, a.kv_len) : a.kv_len;
 
   const int key_end = wave_uniform(decode_key_end(0, kQ16, a.q_len, a.kv_len, a.bs));
-  const int lo = wave_uniform(split * a.split_len);
-  const int hi = wave_uniform(imin(lo + a.split_len, key_end));
-  const int n_chunks = hi > lo ? (hi - lo + kChunk16 - 1) / kChunk16 : 0;
   // keys below kfull are seen by every row (row 0 has the smallest position)
   const int kfull = wave_uniform(imin(((a.kv_len - a.q_len) / a.bs + 1) * a.bs, a.kv_len));
-
-  f32x4 o[4] = {};  // O^T [16-d block]: lane (row l16, hq) holds d 16db + 4hq + r
-  float m = -INFINITY, lsum = 0.f;
   const int tr_row = l16 >> 2;
   const int tr_col = 4 * (lane & 3);
 
   // lane + 64j -> key row c0 + lane/8 + 8j, 16-byte part lane%8
   u32x4 kr[kLoads16], vr[kLoads16];
-  // Wave step i handles chunk (i + r0) mod n_chunks. Without the rotation every
-  // workgroup reads the same offset of its head's K/V at the same time, and the
-  // head stride (kv_len x 128 bytes) piles those reads onto few HBM channels;
-  // starting head bh at chunk 7 bh spreads them (measured 71 -> 66 us at
-  // 32 x 12 heads, kv_len 4112, one split).
-  const int r0 = wave_uniform(n_chunks > 0 ? (bh * 7) % n_chunks : 0);
-  auto rot = [&](int i) { const int c = i + r0; return c >= n_chunks ? c - n_chunks : c; };
-  auto load = [&](int ch) {
-    const int c0 = lo + rot(ch) * kChunk16;
+  auto load = [&](int c0) {
 #pragma unroll
     for (int j = 0; j < kLoads16; ++j) {
       const int key = imin(c0 + (lane >> 3) + 8 * j, a.kv_len - 1);
@@ -320,17 +306,13 @@ __global__ __launch_bounds__(NW * 64, BD3_DEC16_OCC) void decode16_partial(Decod
       vr[j] = ld16_stream(vp + (int64_t)key * a.sv.s + 8 * (lane & 7));
     }
   };
-  if (wave < n_chunks) load(wave);
-  for (int ch = wave; ch < n_chunks; ch += NW) {
-    const int c0 = lo + rot(ch) * kChunk16;
-#pragma unroll
-    for (int j = 0; j < kLoads16; ++j) {
-      const int off = ((lane >> 3) + 8 * j) * kStride + 8 * (lane & 7);
-      *reinterpret_cast<u32x4*>(&ks[off]) = kr[j];
-      *reinterpret_cast<u32x4*>(&vs[off]) = vr[j];
-    }
-    // The wave's next chunk streams in while this one is computed from LDS.
-    if (ch + NW < n_chunks) load(ch + NW);
+
+  // One 32-key chunk starting at c0 (keys from hi on are the next split's or
+  // invisible), already in the wave's LDS tiles, into the online-softmax
+  // state (m, lsum, o): lsum is the lane's share of the row sum (its 8 keys
+  // per chunk), o is O^T unnormalised ([16-d block]: lane (row l16, hq) holds
+  // d 16db + 4hq + r).
+  auto chunk = [&](int c0, int hi, float& m, float& lsum, f32x4 (&o)[4]) {
     f32x4 s[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
@@ -376,6 +358,107 @@ __global__ __launch_bounds__(NW * 64, BD3_DEC16_OCC) void decode16_partial(Decod
                              lds_read_tr(&vs[(row + 16) * kStride + 16 * db + tr_col]));
       o[db] = mfma16(va, pop, o[db]);
     }
+  };
+  // The chunk loaded last (registers) to the wave's LDS tiles.
+  auto stage = [&]() {
+#pragma unroll
+    for (int j = 0; j < kLoads16; ++j) {
+      const int off = ((lane >> 3) + 8 * j) * kStride + 8 * (lane & 7);
+      *reinterpret_cast<u32x4*>(&ks[off]) = kr[j];
+      *reinterpret_cast<u32x4*>(&vs[off]) = vr[j];
+    }
+  };
+  // Chunk i of a split's walk is chunk (i + r0) mod n_chunks of the split
+  // (r0 = 7 bh mod n_chunks, the same for every wave). Without that rotation
+  // every workgroup reads the same offset of its head's K/V at the same
+  // time, and the head stride (kv_len x 128 bytes) piles those reads onto
+  // few HBM channels; starting head bh at chunk 7 bh spreads them (measured
+  // 71 -> 66 us at 32 x 12 heads, kv_len 4112, one split).
+  auto split_lo = [&](int sp) { return wave_uniform(sp * a.split_len); };
+  auto split_hi = [&](int sp) { return wave_uniform(imin(sp * a.split_len + a.split_len, key_end)); };
+  auto n_chunks_of = [&](int sp) {
+    const int lo = split_lo(sp), hi = split_hi(sp);
+    return hi > lo ? (hi - lo + kChunk16 - 1) / kChunk16 : 0;
+  };
+  auto chunk_c0 = [&](int sp, int nc, int i) {
+    const int c = i + (nc > 0 ? (bh * 7) % nc : 0);
+    return split_lo(sp) + (c >= nc ? c - nc : c) * kChunk16;
+  };
+
+  // The wave's state for the workgroup merge: weights 2^(m - max m), sums l,
+  // unnormalised O (lane shares of l, summed below).
+  f32x4 o[4] = {};
+  float m = -INFINITY, lsum = 0.f;
+  const int s0 = wave_uniform(grp * a.splits_per_group);
+  const int s1 = wave_uniform(imin(s0 + a.splits_per_group, a.n_splits));
+  if (a.splits_per_group == 1) {
+    // One split per workgroup: the waves take its chunks in turn; each
+    // wave's next chunk streams in while the current one is computed.
+    const int hi = split_hi(s0);
+    const int nc = n_chunks_of(s0);
+    if (wave < nc) load(chunk_c0(s0, nc, wave));
+    for (int ch = wave; ch < nc; ch += NW) {
+      stage();
+      if (ch + NW < nc) load(chunk_c0(s0, nc, ch + NW));
+      chunk(chunk_c0(s0, nc, ch), hi, m, lsum, o);
+    }
+  } else {
+    // Several splits per workgroup, computed one after another; the waves
+    // take the chunks in turn (the one-split read pattern). A
+    // wave's share of a split gives a normalised partial and its log2-LSE
+    // (the reference's per-split result, kernels/SplitKVDecodeAttention.py:
+    // 81-87, over the wave's keys of the split), merged into the wave's
+    // running state with the reference's LSE weights (:109-127); the
+    // workgroup merge below combines the waves the same way. The lane shares
+    // of l stay unreduced: m and O are per row, the weights apply to every
+    // share. The next chunk's loads (at a split's end, the wave's first
+    // chunk of the next split) stream in while the current chunk is computed.
+    // The workgroup's chunks, split after split, are dealt to the waves in
+    // turn (chunk g of the sequence to wave g mod NW), so every wave gets the
+    // same count to within one whatever the chunks per split.
+    int sp = s0, nc = n_chunks_of(s0), i = wave;
+    while (sp < s1 && i >= nc) {
+      i -= nc;
+      ++sp;
+      nc = sp < s1 ? n_chunks_of(sp) : 0;
+    }
+    if (sp < s1) load(chunk_c0(sp, nc, i));
+    float ms = -INFINITY, ls = 0.f;
+    f32x4 os[4] = {};
+    while (sp < s1) {
+      stage();
+      int sp_n = sp, nc_n = nc, i_n = i + NW;
+      while (sp_n < s1 && i_n >= nc_n) {
+        i_n -= nc_n;
+        ++sp_n;
+        nc_n = sp_n < s1 ? n_chunks_of(sp_n) : 0;
+      }
+      if (sp_n < s1) load(chunk_c0(sp_n, nc_n, i_n));
+      chunk(chunk_c0(sp, nc, i), split_hi(sp), ms, ls, os);
+      if (sp_n != sp) {
+        // the wave's share of split sp is done: merge its normalised partial
+        float lrow = ls + shfl_xor(ls, 16);
+        lrow = sum_xor32(lrow);
+        if (lrow > 0.f) {
+          const float lse = ms + fast_log2(lrow);  // log2-LSE of the share
+          const float mn = fmaxf(m, lse);
+          const float w_old = m == -INFINITY ? 0.f : fast_exp2(m - mn);
+          const float w_new = fast_exp2(lse - mn) / lrow;  // weight of the normalised partial
+          m = mn;
+          // running state: each of the row's 4 lane shares holds a quarter of l
+          lsum = lsum * w_old + 0.25f * fast_exp2(lse - mn);
+#pragma unroll
+          for (int db = 0; db < 4; ++db) o[db] = o[db] * w_old + os[db] * w_new;
+        }
+        ms = -INFINITY;
+        ls = 0.f;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) os[db] = f32x4{};
+      }
+      sp = sp_n;
+      nc = nc_n;
+      i = i_n;
+    }
   }
 
   // Merge the waves' states.
@@ -410,7 +493,7 @@ __global__ __launch_bounds__(NW * 64, BD3_DEC16_OCC) void decode16_partial(Decod
 #pragma unroll
     for (int j = 0; j < kOut; ++j) ot[j] += wgt * ml->o[w][d0 + j][row];
   }
-  if (a.n_splits == 1) {
+  if (a.groups == 1) {
     if (row < a.q_len) {
       const float inv = 1.f / lt;
       uint16_t* dst = a.o + b * a.so.b + h * a.so.h + (int64_t)row * a.so.s + d0;
@@ -425,7 +508,7 @@ __global__ __launch_bounds__(NW * 64, BD3_DEC16_OCC) void decode16_partial(Decod
       }
     }
   } else {
-    const int64_t slot = (int64_t)bh * a.q_tiles * a.n_splits + split;  // q_tiles == 1
+    const int64_t slot = (int64_t)bh * a.q_tiles * a.groups + grp;  // q_tiles == 1
     const float inv = lt > 0.f ? 1.f / lt : 0.f;
     float* dst = &a.part_o[(slot * kQT + row) * kHeadDim + d0];
 #pragma unroll
@@ -444,7 +527,7 @@ __global__ __launch_bounds__(kThreads) void decode_combine(DecodeArgs a) {
   const int b = bh / a.heads, h = bh - b * a.heads;
   const int i0 = qt * kQT;
   uint16_t* op = a.o + b * a.so.b + h * a.so.h;
-  const int64_t slot0 = ((int64_t)bh * a.q_tiles + qt) * a.n_splits;
+  const int64_t slot0 = ((int64_t)bh * a.q_tiles + qt) * a.groups;
   const int d0 = 4 * (threadIdx.x & 15);
 #pragma unroll
   for (int pass = 0; pass < kQT / 16; ++pass) {
@@ -475,7 +558,7 @@ __global__ __launch_bounds__(kThreads) void decode_combine(DecodeArgs a) {
       // issued before the first use); the same weights, summed in split
       // order.
       constexpr int kG = 8;
-      const int ns = a.n_splits;
+      const int ns = a.groups;
       for (int s0 = 0; s0 < ns; s0 += kG) {
         float l[kG];
 #pragma unroll
@@ -526,15 +609,15 @@ __global__ void mask_dump_kernel(uint8_t* out, int mode, int rows, int cols, int
 }  // namespace
 
 hipError_t launch_decode(const DecodeArgs& a, int /*qt*/, hipStream_t stream) {
-  dim3 grid(a.n_splits, a.q_tiles, a.bh);
+  dim3 grid(a.groups, a.q_tiles, a.bh);
   if (a.q_len <= kQ16)
     hipLaunchKernelGGL(decode16_partial<kNW>, grid, dim3(kThreads), 0, stream, a);
   else
     hipLaunchKernelGGL(decode_partial, grid, dim3(kThreads), 0, stream, a);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || a.n_splits == 1) return e;
+  if (e != hipSuccess || a.groups == 1) return e;
   const dim3 cgrid(a.q_tiles, a.bh);
-  switch (a.n_splits) {
+  switch (a.groups) {
     case 2: hipLaunchKernelGGL(decode_combine<2>, cgrid, dim3(kThreads), 0, stream, a); break;
     case 3: hipLaunchKernelGGL(decode_combine<3>, cgrid, dim3(kThreads), 0, stream, a); break;
     case 4: hipLaunchKernelGGL(decode_combine<4>, cgrid, dim3(kThreads), 0, stream, a); break;
