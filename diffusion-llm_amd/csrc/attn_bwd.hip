@@ -146,39 +146,41 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dkdv_dma_kernel(BwdArgs a) 
 
   f32x16 dk[2] = {}, dv[2] = {};  // [d block]: lane = d column, registers = keys
 
-  // P^T and -dS^T operands of one 32-row block qb of the current query tile:
-  // S, Delta - dP (rows x keys, lane = key column, register r <-> row
-  // 32qb + 8(r/4) + 4g + r%4), P, -dS. A block that is not fully visible gets
-  // P = 0 on its invisible pairs: with MASK16 (block size a multiple of 16)
-  // the mask is constant on 16-row x 1-key strips, so one test per lane for
-  // rows 0-15 of the block (registers 0-7) and one for rows 16-31 decide it;
-  // otherwise every pair is tested. A dead block is computed and fully masked.
-  auto block_ops = [&](const __bf16* qs, const __bf16* dos, const float* scal, int q0, int qb, bool masked,
-                       bf16x8 (&pop)[2], bf16x8 (&dsop)[2]) {
-    bf16x8 qa[4], da[4];
+  // Scores and Delta - dP of the 32-row blocks of the current query tile
+  // (rows x keys, lane = key column, register r <-> row 32qb + 8(r/4) + 4g +
+  // r%4): the chains start from the rows' L * log2(e) and Delta, read from the
+  // tile's row scalars in accumulator order. The two blocks' four chains are
+  // issued interleaved, so no product waits for the one before it.
+  auto products = [&](const __bf16* qs, const __bf16* dos, const float* scal, f32x16 (&s)[2], f32x16 (&dp)[2]) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      qa[c] = sw_row_op(qs, 32 * qb, c, lane);
-      da[c] = sw_row_op(dos, 32 * qb, c, lane);
-    }
-    // The rows' Delta and L * log2(e), in accumulator order, as the starts
-    // of the dP and score chains.
-    f32x16 dp, s;
+    for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-    for (int rg = 0; rg < 4; ++rg) {
-      const f32x4 dr = *reinterpret_cast<const f32x4*>(&scal[64 + 32 * qb + 8 * rg + 4 * g]);
-      const f32x4 lr = *reinterpret_cast<const f32x4*>(&scal[32 * qb + 8 * rg + 4 * g]);
+      for (int rg = 0; rg < 4; ++rg) {
+        const f32x4 dr = *reinterpret_cast<const f32x4*>(&scal[64 + 32 * qb + 8 * rg + 4 * g]);
+        const f32x4 lr = *reinterpret_cast<const f32x4*>(&scal[32 * qb + 8 * rg + 4 * g]);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        dp[4 * rg + j] = dr[j];
-        s[4 * rg + j] = lr[j];
+        for (int j = 0; j < 4; ++j) {
+          dp[qb][4 * rg + j] = dr[j];
+          s[qb][4 * rg + j] = lr[j];
+        }
       }
-    }
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      s = mfma32(qa[c], kreg[c], s);     // L * log2(e) - S * scale * log2(e)
-      dp = mfma32(da[c], vreg[c], dp);  // Delta - dP (V negated)
-    }
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        s[qb] = mfma32(sw_row_op(qs, 32 * qb, c, lane), kreg[c], s[qb]);     // L log2(e) - S scale log2(e)
+        dp[qb] = mfma32(sw_row_op(dos, 32 * qb, c, lane), vreg[c], dp[qb]);  // Delta - dP (V negated)
+      }
+  };
+
+  // P^T and -dS^T operands of block qb: P = exp2(-s), -dS = P o (Delta -
+  // dP). A block that is not fully visible gets P = 0 on its invisible
+  // pairs: with MASK16 (block size a multiple of 16) the mask is constant on
+  // 16-row x 1-key strips, so one test per lane for rows 0-15 of the block
+  // (registers 0-7) and one for rows 16-31 decide it; otherwise every pair
+  // is tested. A dead block is computed and fully masked.
+  auto softmax_ops = [&](const f32x16& s, const f32x16& dp, int q0, int qb, bool masked, bf16x8 (&pop)[2],
+                         bf16x8 (&dsop)[2]) {
     float p[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) p[r] = fast_exp2(-s[r]);
@@ -221,8 +223,10 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dkdv_dma_kernel(BwdArgs a) 
       const __bf16* dos = qs + kSwTile;
       const float* scal = reinterpret_cast<const float*>(qs + 2 * kSwTile);
       bf16x8 pop[2][2], dsop[2][2];  // [row block][16-row step]
-      block_ops(qs, dos, scal, q0, 0, c0 != kFull, pop[0], dsop[0]);
-      block_ops(qs, dos, scal, q0, 1, c1 != kFull, pop[1], dsop[1]);
+      f32x16 sc[2], dpc[2];
+      products(qs, dos, scal, sc, dpc);
+      softmax_ops(sc[0], dpc[0], q0, 0, c0 != kFull, pop[0], dsop[0]);
+      softmax_ops(sc[1], dpc[1], q0, 1, c1 != kFull, pop[1], dsop[1]);
       // dV += P^T dO, dK += dS^T Q with dO / Q read transposed.
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb)
@@ -457,6 +461,7 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dq_dma_kernel(BwdArgs a) {
 #ifndef BD3_KV_OCC
 #define BD3_KV_OCC 2
 #endif
+
 
 }  // namespace
 
