@@ -145,26 +145,28 @@ class TrainStep:
 
 
 def _capture_step(step: TrainStep):
-    """One training step (forward, dQ, dK/dV launches) captured as a HIP
-    graph on a side stream. Returns the graph, or None when capture is not
-    available; the caller then launches the kernels eagerly."""
+    """The forward and the backward (dQ + dK/dV launches) captured as two HIP
+    graphs on a side stream. Returns (forward replay, backward replay), or
+    None when capture is not available; the caller then launches the kernels
+    eagerly."""
     import torch
+    saved = step.stream
     try:
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
-        graph = torch.cuda.CUDAGraph()
-        saved = step.stream
+        graphs = (torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph())
         with torch.cuda.stream(side):
             step.stream = torch.cuda.current_stream().cuda_stream
             step.fwd()
             step.bwd()
             torch.cuda.synchronize()
-            with torch.cuda.graph(graph, stream=side):
+            with torch.cuda.graph(graphs[0], stream=side):
                 step.fwd()
+            with torch.cuda.graph(graphs[1], stream=side):
                 step.bwd()
         step.stream = saved
         torch.cuda.synchronize()
-        return graph
+        return graphs[0].replay, graphs[1].replay
     except Exception as exc:  # capture unsupported: eager launches
         log(f"graph capture unavailable ({exc}); timing eager launches")
         step.stream = saved
@@ -174,19 +176,24 @@ def _capture_step(step: TrainStep):
 
 def time_train(step: TrainStep, steps: int, warmup: int, use_graph: bool = False, ramp_s: float = 2.0):
     """Ramp the clocks (eager steps for ramp_s seconds), run `warmup`
-    untimed steps, then time exactly `steps` fwd+bwd steps: wall clock between
-    two synchronisations, each step being the forward, dQ and dK/dV launches
-    on one stream (or replayed from one captured HIP graph: on this stack a
-    freshly captured graph's replays run 5-25% slower than the same launches
-    made directly, for the first few graphs of a process). Separately,
-    each kernel's launch duration: HIP events on the launch stream around
-    `steps` back-to-back launches of that kernel alone.
-    Returns (ms per step, ms per launch of each kernel, launch mode)."""
+    untimed steps, then time exactly `steps` fwd+bwd steps between two
+    synchronisations, in the reference microbench's protocol
+    (bench/attention_bench.py:61-76 with bench/harness.py:25-51): the caches
+    are evicted (a 1 GiB read, larger than the 256 MB Infinity Cache) before
+    the forward and again before the backward, and HIP events on the launch
+    stream time each; fwd+bwd is their sum. Events also separate the
+    backward's two kernels (dQ, dK/dV). With `use_graph` the forward and the
+    backward are replayed from two captured HIP graphs. The same steps are
+    also timed back to back without eviction (wall clock) for comparison.
+
+    Returns a dict: step_ms (median, p20, p80, mean of fwd + bwd over the
+    timed steps), kernel_ms (median of each kernel), warm_ms_per_step,
+    launch."""
     import torch
+    from perf.harness import Samples, flush_caches
     # Ramp: on a freshly started process the step runs ~15% slow for the
     # first ~1.5 s of load (clocks and first touches settling), far longer
-    # than W warm-up steps last. Eager steps for at least ramp_s seconds come
-    # before the W warm-up steps.
+    # than W warm-up steps last.
     t_end = time.perf_counter() + ramp_s
     while time.perf_counter() < t_end:
         for _ in range(20):
@@ -197,27 +204,58 @@ def time_train(step: TrainStep, steps: int, warmup: int, use_graph: bool = False
         step.fwd()
         step.bwd()
     torch.cuda.synchronize()
-    graph = _capture_step(step) if use_graph else None
-    run = graph.replay if graph is not None else (lambda: (step.fwd(), step.bwd()))
-    for _ in range(warmup):
-        run()
+    graphs = _capture_step(step) if use_graph else None
+    fwd_fn, bwd_fn = graphs if graphs is not None else (step.fwd, step.bwd)
+    stream = torch.cuda.current_stream()
+    events = []
+    torch.cuda.synchronize()
+    for _ in range(steps):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
+        flush_caches()
+        ev[0].record(stream)
+        fwd_fn()
+        ev[1].record(stream)
+        flush_caches()
+        ev[2].record(stream)
+        if graphs is None:
+            step.bwd_dq()
+            ev[3].record(stream)
+            step.bwd_dkdv()
+        else:
+            bwd_fn()
+            ev[3].record(stream)
+        ev[4].record(stream)
+        events.append(ev)
+    torch.cuda.synchronize()
+    total = Samples([e[0].elapsed_time(e[1]) + e[2].elapsed_time(e[4]) for e in events])
+    kernel_ms = {"fwd": Samples([e[0].elapsed_time(e[1]) for e in events]).median_ms,
+                 "bwd": Samples([e[2].elapsed_time(e[4]) for e in events]).median_ms}
+    if graphs is None:
+        kernel_ms["bwd_dq"] = Samples([e[2].elapsed_time(e[3]) for e in events]).median_ms
+        kernel_ms["bwd_dkdv"] = Samples([e[3].elapsed_time(e[4]) for e in events]).median_ms
+    # the same steps back to back, caches warm, wall clock
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
-        run()
+        fwd_fn()
+        bwd_fn()
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    per = {}
-    for name, fn in (("fwd", step.fwd), ("bwd_dq", step.bwd_dq), ("bwd_dkdv", step.bwd_dkdv)):
-        fn()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(steps):
-            fn()
-        e1.record()
-        torch.cuda.synchronize()
-        per[name] = e0.elapsed_time(e1) / steps
-    return wall * 1e3 / steps, per, ("hip_graph" if graph is not None else "eager")
+    warm = (time.perf_counter() - t0) * 1e3 / steps
+    return {"step_ms": {"median": total.median_ms, "p20": total.p20_ms, "p80": total.p80_ms,
+                        "mean": total.mean_ms},
+            "kernel_ms": kernel_ms, "warm_ms_per_step": warm,
+            "launch": "hip_graph" if graphs is not None else "eager"}
+
+
+def host_threads() -> dict:
+    """Give torch's CPU ops os.cpu_count() threads (BASELINE.md's CPU plan)
+    and return the counts: the threads used, the cores this process may run
+    on (affinity) and the machine's total logical cores."""
+    import torch
+    total = os.cpu_count() or 1
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else total
+    torch.set_num_threads(total)
+    return {"threads": torch.get_num_threads(), "affinity_cores": affinity, "total_cores": total}
 
 
 def cpu_baseline(B, H, n, bs, budget_s: float):
@@ -225,9 +263,7 @@ def cpu_baseline(B, H, n, bs, budget_s: float):
     budget is spent; value in useful TFLOP/s (same FLOP convention)."""
     import torch
     from oracle.attention import bd3_attention_grads
-    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    cores = max(1, min(cores, 16))
-    torch.set_num_threads(cores)
+    cores = host_threads()
     g = torch.Generator().manual_seed(0)
     q, k, v, do = (torch.randn(1, 1, 2 * n, D, generator=g).to(torch.bfloat16).float() for _ in range(4))
     bd3_attention_grads(q, k, v, do, bs)  # warmup (allocations)
@@ -261,10 +297,11 @@ def cpu_baseline(B, H, n, bs, budget_s: float):
     return {
         "value": flops / el / 1e12,
         "unit": "TFLOP/s",
-        "cores": cores,
+        "cores": cores["threads"],
+        "host": cores,
         "kind": "port",
         "sample": (f"{done} of {B * H} (b,h) slices of the B={B} L={n} H={H} bs={bs} workload, "
-                   f"fp32 eager fwd+bwd (torch autograd, {cores} threads, {cpu_model}); "
+                   f"fp32 eager fwd+bwd (torch autograd, {cores['threads']} threads, {cpu_model}); "
                    f"{el:.1f} s"),
         "fwd_value": useful_fwd_flops(1, 1, n, bs) * f_done / f_el / 1e12,
         "fwd_sample": f"{f_done} (b,h) slices, fp32 eager forward only; {f_el:.1f} s",
@@ -277,9 +314,7 @@ def decode_cpu_baseline(budget_s: float):
     spent; value in K+V GB/s (the GPU metric's byte convention)."""
     import torch
     from oracle.attention import decode_attention
-    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    cores = max(1, min(cores, 16))
-    torch.set_num_threads(cores)
+    cores = host_threads()
     H, q_len, kv_len, bs = 12, 16, 4112, 16
     g = torch.Generator().manual_seed(0)
     q = torch.randn(1, H, q_len, D, generator=g).to(torch.bfloat16).float()
@@ -294,7 +329,7 @@ def decode_cpu_baseline(budget_s: float):
             if el >= budget_s or done >= 32:
                 break
     nbytes = 2 * H * kv_len * D * 2 * done
-    return {"value": nbytes / el / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
+    return {"value": nbytes / el / 1e9, "unit": "GB/s", "cores": cores["threads"], "host": cores, "kind": "port",
             "sample": f"{done} of 32 sequences (12 heads each) of configs[3], fp32 eager decode; {el:.2f} s"}
 
 
@@ -350,6 +385,37 @@ def decode_bench(device, reps: int):
                      "frac": best["GB_s"] / PEAK_HBM_GBS, "traffic": measured_traffic("decode16_partial"),
                      "kernel": f"bd3_decode_splitkv n_splits={best['n_splits']} ({best['rule']})"},
     }
+
+
+def decode_b1_bench(device, reps: int):
+    """The reference's decode profiling shapes (bench/decode_ncu.py:16-19):
+    batch 1, 12 heads, block 16; `cached`: a 16-token block over a 3584-token
+    cache, `uncached`: the whole 3088-token sequence block-causal. Each through
+    the bsdfa path (bd3_decode, automatic split count) and the split_kv path
+    (the reference rule: ceil(kv_len / 256) splits, prefill falls back to
+    bsdfa as the reference does, kernels/SplitKVDecodeAttention.py:140-147).
+    HIP events, 1 GiB cache eviction before each call; KV-read GB/s counts the
+    K and V bytes the rows can see."""
+    import torch
+    from kernels.BlockSparseDecodeAttention import block_sparse_decode_attention
+    from kernels.SplitKVDecodeAttention import split_kv_decode_attention
+    from kernels._native import lib
+    from perf.harness import bench
+    out = {}
+    for shape, (q_len, kv_len) in (("cached", (16, 3584)), ("uncached", (3088, 3088))):
+        (q,) = seeded_bf16((1, 12, q_len, D), 3, 1, device)
+        k, v = seeded_bf16((1, 12, kv_len, D), 4, 2, device)
+        kv_bytes = 2 * 12 * kv_len * D * 2
+        for name, fn, splits in (
+                ("bsdfa", block_sparse_decode_attention, lib().bd3_decode_auto_splits(1, 12, q_len, kv_len)),
+                ("split_kv", split_kv_decode_attention, -(-kv_len // 256) if q_len <= 64 else "bsdfa fallback")):
+            t = bench(lambda: fn(q, k, v, 16), warmup=5, rep=reps, flush=True)
+            out[f"{shape}_{name}"] = {"q_len": q_len, "kv_len": kv_len, "heads": 12, "n_splits": splits,
+                                      "us": t.median_ms * 1e3, "us_p20": t.p20_ms * 1e3, "us_p80": t.p80_ms * 1e3,
+                                      "kv_GB_s": kv_bytes / (t.median_ms * 1e-3) / 1e9}
+        del q, k, v
+        torch.cuda.empty_cache()
+    return out
 
 
 def kvcache_bench(device, reps: int):
@@ -531,20 +597,74 @@ def glue_bench(device, reps: int):
     return out
 
 
+def census(n, bs):
+    """Useful and executed pairs per (b, h) of each training kernel's
+    schedule (bd3_train_tile_census)."""
+    from kernels._native import lib
+    out = (ctypes.c_int64 * 8)()
+    lib().bd3_train_tile_census(n, bs, out)
+    return {"useful_pairs": out[0], "executed_pairs": {"fwd": out[1], "bwd_dq": out[6], "bwd_dkdv": out[7]},
+            "useful_fraction_of_executed": {"fwd": out[0] / out[1], "bwd_dq": out[0] / out[6],
+                                            "bwd_dkdv": out[0] / out[7]}}
+
+
+def train_record(step: "TrainStep", t: dict) -> dict:
+    """Throughput figures of one timed training configuration.
+
+    useful: 3.5 x the useful forward FLOPs 4*d*B*H*(n^2 + n*bs) per step
+    (backward credited 2.5x forward, bench/attention_bench.py:89,99, counted on
+    unmasked pairs only). reference_convention: the reference microbench's
+    own figures, dense FLOPs 4*B*H*L^2*d with L = 2n, fwd_tflops =
+    fwd_flops / fwd time, bwd_tflops = 2.5 fwd_flops / bwd time
+    (bench/attention_bench.py:89,98-99). kernel_formed_tflops: the products
+    each kernel forms (forward S, PV; dQ kernel S, dP, dQ; dK/dV kernel S, dP,
+    dV, dK: recomputation included) per second."""
+    B, H, n, bs = step.B, step.H, step.n, step.bs
+    fwd = useful_fwd_flops(B, H, n, bs)
+    ms = t["step_ms"]["median"]
+    rec = {"ms_per_step": ms, "step_ms": t["step_ms"], "warm_ms_per_step": t["warm_ms_per_step"],
+           "launch": t["launch"], "kernel_ms": t["kernel_ms"],
+           "useful_tflops": 3.5 * fwd / (ms * 1e-3) / 1e12,
+           "frac_of_peak": 3.5 * fwd / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+           "census": census(n, bs)}
+    km = t["kernel_ms"]
+    if km:
+        dense = 4 * B * H * (2 * n) ** 2 * D
+        bwd_ms = km["bwd"]
+        rec["useful_fwd_tflops"] = fwd / (km["fwd"] * 1e-3) / 1e12
+        rec["useful_bwd_tflops"] = 2.5 * fwd / (bwd_ms * 1e-3) / 1e12
+        rec["reference_convention"] = {"fwd_ms": km["fwd"], "bwd_ms": bwd_ms, "dense_fwd_flops": dense,
+                                       "fwd_tflops": dense / (km["fwd"] * 1e-3) / 1e12,
+                                       "bwd_tflops": 2.5 * dense / (bwd_ms * 1e-3) / 1e12}
+        formed = {"fwd": 1.0, "bwd_dq": 1.5, "bwd_dkdv": 2.0}
+        rec["kernel_formed_tflops"] = {k: formed[k] * fwd / (km[k] * 1e-3) / 1e12 for k in formed if k in km}
+    return rec
+
+
 def sweep_bench(device, steps: int, use_graph: bool = False):
     """B=4, L=2048, H=16, block sizes {4, 16, 64, 256}."""
     import torch
-    from kernels._native import lib
     out = []
-    census = (ctypes.c_int64 * 6)()
     for bs in (4, 16, 64, 256):
         st = TrainStep(4, 16, 2048, bs, device)
-        ms, per, launch = time_train(st, steps, 2, use_graph, ramp_s=0.3)
-        lib().bd3_train_tile_census(2048, bs, census)
-        out.append({"block_size": bs, "ms": ms, "launch": launch, "kernel_ms": per,
-                    "useful_tflops": st.useful_flops() / (ms * 1e-3) / 1e12,
-                    "frac_of_peak": st.useful_flops() / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
-                    "useful_fraction_of_executed": census[0] / census[1]})
+        t = time_train(st, steps, 2, use_graph, ramp_s=0.3)
+        out.append({"block_size": bs, **train_record(st, t)})
+        del st
+        torch.cuda.empty_cache()
+    return out
+
+
+def long_bench(device, steps: int):
+    """The reference microbench's sequence ladder (bench/attention_bench.py:
+    15-20, :86): 16384 tokens per batch, B = 16384 / 2n, 12 heads, n in
+    {1024, 2048, 4096, 8192} at block 16 and n = 4096 at blocks {4, 64, 256}."""
+    import torch
+    out = []
+    for n, bs in [(1024, 16), (2048, 16), (4096, 16), (8192, 16), (4096, 4), (4096, 64), (4096, 256)]:
+        B = max(1, 16384 // (2 * n))
+        st = TrainStep(B, 12, n, bs, device)
+        t = time_train(st, steps, 2, False, ramp_s=0.3)
+        out.append({"n": n, "attn_seq": 2 * n, "batch": B, "block_size": bs, **train_record(st, t)})
         del st
         torch.cuda.empty_cache()
     return out
@@ -559,6 +679,7 @@ def main(argv=None) -> int:
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--long", action="store_true", help="also time the reference microbench's long-sequence ladder")
     ap.add_argument("--no-kvcache", action="store_true")
     ap.add_argument("--no-sampling", action="store_true")
     ap.add_argument("--no-glue", action="store_true")
@@ -580,24 +701,28 @@ def main(argv=None) -> int:
 
     B, H, n, bs = 8, 12, 1024, 16
     step = TrainStep(B, H, n, bs, device)
-    ms, per, launch = time_train(step, args.steps, args.warmup, use_graph=args.graph)
-    tflops = step.useful_flops() / (ms * 1e-3) / 1e12
-    log(f"config1 fwd+bwd ({launch}): {ms * 1e3:.1f} us/step (fwd {per['fwd'] * 1e3:.1f} us, "
-        f"dQ {per['bwd_dq'] * 1e3:.1f} us, dK/dV {per['bwd_dkdv'] * 1e3:.1f} us) -> {tflops:.1f} useful TFLOP/s")
+    t = time_train(step, args.steps, args.warmup, use_graph=args.graph)
+    rec = train_record(step, t)
+    ms, per = rec["ms_per_step"], t["kernel_ms"]
+    tflops = rec["useful_tflops"]
+    log(f"config1 fwd+bwd ({t['launch']}, caches evicted before fwd and before bwd): {ms * 1e3:.1f} us/step median "
+        f"(p20 {t['step_ms']['p20'] * 1e3:.1f}, p80 {t['step_ms']['p80'] * 1e3:.1f}; back to back warm "
+        f"{t['warm_ms_per_step'] * 1e3:.1f}) -> {tflops:.1f} useful TFLOP/s")
+    if "bwd_dq" in per:
+        log(f"  fwd {per['fwd'] * 1e3:.1f} us, dQ {per['bwd_dq'] * 1e3:.1f} us, dK/dV {per['bwd_dkdv'] * 1e3:.1f} us")
 
-    # Algorithmic FLOPs per launch: 2*d per live pair per matrix product the
-    # kernel must form (forward: S, PV; dQ kernel: S, dP, dQ; dK/dV kernel:
-    # S, dP, dV, dK).
+    # Dominant kernel's roofline: its algorithmic (useful) FLOPs per launch,
+    # the FA2 credit of the products it owns (forward 1x the useful forward
+    # FLOPs; dQ kernel 0.5x: the dQ product; dK/dV kernel 2x: S, dP, dV, dK),
+    # over its median launch duration inside the timed steps.
     fwd_flops = useful_fwd_flops(B, H, n, bs)
-    kernels = {
-        "attn_fwd_dma_kernel": (fwd_flops, per["fwd"]),
-        "attn_bwd_dq_dma_kernel": (1.5 * fwd_flops, per["bwd_dq"]),
-        "attn_bwd_dkdv_dma_kernel": (2.0 * fwd_flops, per["bwd_dkdv"]),
-    }
-    dom_name, (dom_flops, dom_ms) = max(kernels.items(), key=lambda kv: kv[1][1])
-    achieved = dom_flops / (dom_ms * 1e-3) / 1e12
-    census = (ctypes.c_int64 * 6)()
-    lib().bd3_train_tile_census(n, bs, census)
+    credit = {"fwd": 1.0, "bwd_dq": 0.5, "bwd_dkdv": 2.0}
+    names = {"fwd": "attn_fwd_dma_kernel", "bwd_dq": "attn_bwd_dq_dma_kernel",
+             "bwd_dkdv": "attn_bwd_dkdv_dma_kernel"}
+    per = {k: v for k, v in per.items() if k in credit}
+    dom = max(per, key=per.get) if per else "bwd_dkdv"
+    dom_flops = credit[dom] * fwd_flops
+    achieved = dom_flops / (per[dom] * 1e-3) / 1e12 if per else None
 
     result = {
         "metric": metric,
@@ -611,16 +736,17 @@ def main(argv=None) -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic: q, k, v, dO ~ N(0,1) from seed 0, bf16, resident in HBM",
+        "data": "synthetic: q, k, v, dO ~ N(0,1) from seed 0, bf16, resident in HBM (caches evicted before the forward and before the backward)",
         "config": {"workload": "BD3-LM training attention fwd+bwd (configs[1])", "batch": B,
                    "seq_len": n, "attn_seq": 2 * n, "heads": H, "head_dim": D, "block_size": bs},
-        "launch": launch,
-        "kernel_ms": per,
-        "kernel_tflops": {k: f / (t * 1e-3) / 1e12 for k, (f, t) in kernels.items()},
-        "useful_fraction_of_executed": census[0] / census[1],
+        **{k: v for k, v in rec.items() if k not in ("ms_per_step",)},
+        "kernel_useful_tflops": ({k: credit[k] * fwd_flops / (per[k] * 1e-3) / 1e12 for k in per} if per else None),
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": measured_traffic(dom_name),
-                     "kernel": dom_name, "algorithmic_flops_per_launch": dom_flops},
+                     "frac": achieved / PEAK_BF16_TFLOPS if achieved else None,
+                     "traffic": measured_traffic(names[dom]),
+                     "kernel": names[dom], "algorithmic_flops_per_launch": dom_flops,
+                     "credit": f"{credit[dom]} x useful forward FLOPs (FA2 convention: backward = 2.5x forward, "
+                               "dQ kernel owns the dQ product, dK/dV kernel S, dP, dV, dK)"},
     }
     del step
     torch.cuda.empty_cache()
@@ -629,6 +755,10 @@ def main(argv=None) -> int:
         result["decode"] = decode_bench(device, reps=30)
         for r in result["decode"]["rows"]:
             log(f"decode n_splits={r['n_splits']:3d} ({r['rule']}): {r['us']:.1f} us, {r['GB_s']:.0f} GB/s")
+    if not args.no_decode:
+        result["decode_batch1"] = decode_b1_bench(device, reps=30)
+        for k_, r in result["decode_batch1"].items():
+            log(f"decode batch-1 {k_}: {r['us']:.1f} us ({r['kv_GB_s']:.0f} GB/s, splits {r['n_splits']})")
     if not args.no_kvcache:
         result["kv_cache"] = kvcache_bench(device, reps=20)
         for k_, r in result["kv_cache"].items():
@@ -650,7 +780,7 @@ def main(argv=None) -> int:
                     f"fused {r['gate_residual_ln_modulate_us']:.1f} us")
     if not args.no_e2e:
         from perf.e2e_sampling import run as e2e_run
-        result["e2e"] = e2e_run(blocks=64, eager_blocks=2, check_steps=6)
+        result["e2e"] = e2e_run(blocks=64, eager_blocks=2, check_steps=4)
         worst = max(d["max_abs"] for d in result["e2e"]["logit_check"])
         log(f"e2e configs[4]: {result['e2e']['tokens_per_s']:.0f} tokens/s "
             f"(reference eager path {result['e2e']['reference_eager_tokens_per_s']:.0f} tokens/s), "
@@ -659,7 +789,13 @@ def main(argv=None) -> int:
     if not args.no_sweep:
         result["sweep"] = sweep_bench(device, steps=10, use_graph=args.graph)
         for r in result["sweep"]:
-            log(f"sweep bs={r['block_size']:3d}: {r['ms'] * 1e3:.1f} us, {r['useful_tflops']:.1f} TFLOP/s")
+            log(f"sweep bs={r['block_size']:3d}: {r['ms_per_step'] * 1e3:.1f} us, {r['useful_tflops']:.1f} TFLOP/s")
+    if args.long:
+        result["long_sequences"] = long_bench(device, steps=10)
+        for r in result["long_sequences"]:
+            log(f"long n={r['n']:5d} B={r['batch']} bs={r['block_size']:3d}: {r['ms_per_step'] * 1e3:.1f} us, "
+                f"{r['useful_tflops']:.1f} useful TFLOP/s; reference convention fwd "
+                f"{r['reference_convention']['fwd_tflops']:.0f} / bwd {r['reference_convention']['bwd_tflops']:.0f} TFLOP/s")
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(B, H, n, bs, args.cpu_budget)

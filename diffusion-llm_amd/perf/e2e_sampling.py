@@ -130,14 +130,19 @@ def rope_eager(x, sin_t, cos_t, positions):
     return torch.cat([x1 * c - x2 * s, x1 * s + x2 * c], dim=-1)
 
 
-def attention_eager(q, k, v):
+def attention_eager(q, k, v, mask=None):
     scores = (q.float() @ k.float().transpose(-1, -2)) / 8.0
+    if mask is not None:
+        scores = torch.where(mask, scores, -torch.inf)
     probs = torch.softmax(scores, dim=-1).to(v.dtype)
     return probs @ v
 
 
-def backbone_eager(cfg, p, tables, block, cache, store):
-    """cache: per layer [k, v] or None (grown with torch.cat, as KVCache)."""
+def backbone_eager(cfg, p, tables, block, cache, store, mask=None):
+    """cache: per layer [k, v] or None (grown with torch.cat, as KVCache).
+    mask: the attention mask of a prefill pass over the whole block (the
+    sampler's prompt pass, sample/sampler.py:80-87, block-causal), or None
+    for a denoising step (every cached and block key visible)."""
     B, S = block.shape
     start = 0 if cache[0] is None else cache[0][0].shape[2]
     positions = torch.arange(start, start + S, device=block.device)
@@ -153,7 +158,7 @@ def backbone_eager(cfg, p, tables, block, cache, store):
             k_all, v_all = torch.cat([cache[li][0], k], dim=2), torch.cat([cache[li][1], v], dim=2)
         if store:
             cache[li] = [k_all, v_all]
-        o = attention_eager(q, k_all, v_all).transpose(1, 2).reshape(B, S, cfg.d)
+        o = attention_eager(q, k_all, v_all, mask).transpose(1, 2).reshape(B, S, cfg.d)
         x = x + g1 * linear(o, L["out"])
         h = ln_eager(x, L["ln2"], cfg.eps) * (1 + sc2) + sh2
         x = x + g2 * linear(F.gelu(linear(h, L["fc1"]), approximate="tanh"), L["fc2"])
@@ -220,7 +225,8 @@ def backbone_bd3(cfg, p, tables, block, cache, store, ada=None):
 
 def generate(cfg, p, tables, batch, n_blocks, steps, backend, check=None, graph=False):
     """sample_bd3lm with the KV cache (sample/sampler.py:37-158). `check`:
-    optional callback(block_idx, step, block, caches) for the logit check.
+    optional callback(block_idx, step, block, caches, committed) for the logit
+    check (committed: the tokens of the blocks before this one).
     graph (bd3 only): the backbone of a block's denoising steps is captured
     once per block as a HIP graph (the cache length, hence every launch
     argument, is fixed within a block) and replayed for each step; the draw
@@ -257,7 +263,7 @@ def generate(cfg, p, tables, batch, n_blocks, steps, backend, check=None, graph=
         for i in range(steps):
             t, s = 1 - i / steps, 1 - (i + 1) / steps
             if check is not None:
-                check(bi, i, block, cache)
+                check(bi, i, block, cache, x)
             if backend == "bd3":
                 if g_step is not None:
                     static_block.copy_(block)
@@ -287,25 +293,35 @@ def run(blocks: int = 64, eager_blocks: int = 2, check_steps: int = 4, batch: in
     tables = rope_tables(cfg.d // cfg.heads, cfg.max_seq, device=device)
     steps = cfg.bs
 
-    # logit check: at sampled steps of the bd3 run, the eager backbone on the
-    # same block over an eager cache holding the same committed tokens.
+    # Logit check: at one denoising step of blocks spread over the run (the
+    # first, the second, the middle and the last block, so the last one runs
+    # against a cache of (blocks - 1) * 32 tokens), the bd3 backbone over its
+    # KV cache against the eager backbone over an eager cache built
+    # independently: one eager prefill pass of the committed tokens,
+    # block-causal (the sampler's prompt pass, sample/sampler.py:78-87; a
+    # prefill gives the same K/V as committing block by block).
     diffs = []
-    check_at = {(b, s) for b in (0, 1, blocks // 2, blocks - 1) for s in (0, steps // 2, steps - 1)}
-    check_at = set(sorted(check_at)[:check_steps]) if check_steps else set()
+    check_blocks = sorted({0, 1, blocks // 2, blocks - 1} & set(range(blocks)))
+    if check_steps < len(check_blocks):  # keep the last block, spread the rest
+        keep = [check_blocks[round(i * (len(check_blocks) - 1) / max(check_steps - 1, 1))]
+                for i in range(check_steps)] if check_steps > 1 else check_blocks[-1:]
+        check_blocks = sorted(set(keep)) if check_steps else []
+    check_at = {(b, steps // 2) for b in check_blocks}
 
-    def check(bi, step, block, cache):
+    def check(bi, step, block, cache, committed):
         if (bi, step) not in check_at:
             return
         with torch.no_grad():
             eager_cache = [None] * cfg.layers
-            if cache.length:
-                for li in range(cfg.layers):
-                    k, v = cache.get(li)
-                    eager_cache[li] = [k.contiguous(), v.contiguous()]
+            P = committed.shape[1]
+            if P:
+                pos = torch.arange(P)
+                causal = ((pos[None, :] // cfg.bs) <= (pos[:, None] // cfg.bs)).to(block.device)
+                backbone_eager(cfg, p, tables, committed, eager_cache, True, mask=causal)
             le = backbone_eager(cfg, p, tables, block, eager_cache, False).float()
             lb = backbone_bd3(cfg, p, tables, block, cache, False).float()
-            diffs.append({"block": bi, "step": step, "max_abs": float((le - lb).abs().max()),
-                          "logit_scale": float(le.abs().max())})
+            diffs.append({"block": bi, "step": step, "cache_tokens": P,
+                          "max_abs": float((le - lb).abs().max()), "logit_scale": float(le.abs().max())})
 
     with torch.no_grad():
         generate(cfg, p, tables, batch, 1, 2, "bd3")  # warm-up

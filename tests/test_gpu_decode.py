@@ -81,3 +81,23 @@ def test_decode_strided_cache_view(cuda):
                                        vc[:, :, :kv_len].contiguous(), bs)
     torch.cuda.synchronize()
     assert torch.equal(o1, o2)
+
+
+# The reference's decode profiling shapes (bench/decode_ncu.py:16-19): batch
+# 1, 12 heads, block 16 -- a 16-token block over a 3584-token cache, and the
+# whole 3088-token sequence block-causal (prefill / uncached step).
+NCU_SHAPES = {"cached": (16, 3584), "uncached": (3088, 3088)}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", sorted(NCU_SHAPES))
+@pytest.mark.parametrize("backend", ["bsdfa", "split_kv"])
+def test_batch1_profiling_shapes(cuda, record_error, shape, backend):
+    q_len, kv_len = NCU_SHAPES[shape]
+    print(f"decode batch-1 {shape} q_len={q_len} kv_len={kv_len} via {backend}", flush=True)
+    q, k, v = decode_inputs(1, 12, q_len, kv_len, seed=kv_len)
+    fn = block_sparse_decode_attention if backend == "bsdfa" else split_kv_decode_attention
+    o = fn(*(t.to(cuda, torch.bfloat16) for t in (q, k, v)), 16)
+    ref = decode_attention(q, k, v, 16)
+    torch.cuda.synchronize()
+    record_error("decode O max-abs", max_abs(o, ref), OUT_TOL)

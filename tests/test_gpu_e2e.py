@@ -1,9 +1,11 @@
-"""configs[4] end to end, shortened: the restated BD3-LM sampler
-(diffusion-llm_amd/perf/e2e_sampling.py) runs with this library's kernels
-on the attention path (fused QKV / RoPE into the KV cache, decode over the
-cache views, LN + modulate, gated residual, SUBS sampling); every [MASK] is
-resolved and the logits at sampled denoising steps match the reference's
-eager backbone on the same tokens and prefix within bf16 rounding."""
+"""configs[4] end to end, shortened to 17 blocks: the restated BD3-LM
+sampler (diffusion-llm_amd/perf/e2e_sampling.py) runs with this library's
+kernels on the attention path (fused QKV / RoPE into the KV cache, decode
+over the cache views, LN + modulate, gated residual, SUBS sampling); every
+[MASK] is resolved and, at a denoising step of blocks 0, 1, 8 and 16 (the
+last against a 512-token cache), the logits match the reference's eager
+backbone over an eager cache built by an independent prefill of the
+committed tokens, within bf16 rounding."""
 from __future__ import annotations
 
 import pytest
@@ -12,10 +14,11 @@ import pytest
 @pytest.mark.gpu
 def test_e2e_sampling_logits_match_eager(cuda):
     from perf.e2e_sampling import run
-    r = run(blocks=2, eager_blocks=1, check_steps=4)
+    r = run(blocks=17, eager_blocks=1, check_steps=4)
     assert r["tokens_per_s"] > 0 and r["reference_eager_tokens_per_s"] > 0
     assert r["graph_tokens_equal_eager_launch"]  # graph replays draw the very same tokens
-    assert len(r["logit_check"]) == 4
+    assert [d["block"] for d in r["logit_check"]] == [0, 1, 8, 16]
+    assert r["logit_check"][-1]["cache_tokens"] == 16 * 32
     for d in r["logit_check"]:
         # 12 bf16 layers: a few bf16 ulps of the logit scale (2^-8 relative each)
         assert d["max_abs"] <= 4 * 2.0 ** -8 * max(d["logit_scale"], 1e-3), d
