@@ -44,16 +44,13 @@ constexpr float kRescale = 8.0f;
 #ifndef BD3_FWD_OCC
 #define BD3_FWD_OCC 3
 #endif
-#ifndef BD3_FWD_HALF
-#define BD3_FWD_HALF 0
-#endif
 #ifndef BD3_FWD_STAGES
 #define BD3_FWD_STAGES 3
 #endif
 
-// One class per 64-key tile for the wave (dead / full / partial, from the
-// row group's thresholds): a full tile runs straight-line code with no mask
-// arithmetic. MASK16: the block size is a multiple of 16.
+// One class per 64-key tile for the wave (dead / full / partial, as walk
+// index intervals of its row group): a full tile runs straight-line code with
+// no mask arithmetic. MASK16: the block size is a multiple of 16.
 template <int OCC, bool MASK16>
 __global__ __launch_bounds__(256, OCC) void attn_fwd_dma_kernel(FwdArgs a) {
   constexpr int kBM = 128;  // query rows per workgroup: 4 waves x 32
@@ -132,7 +129,8 @@ __global__ __launch_bounds__(256, OCC) void attn_fwd_dma_kernel(FwdArgs a) {
 #pragma unroll
   for (int c = 0; c < 4; ++c) qreg[c] = scale_bf16x8(qreg[c], a.scale_log2);
   const RowIntervals riv = train_row_intervals(myq, a.n, a.bs);
-  const ClassBounds cb = uniform_bounds(row_group_bounds(train_row_group(qrow0, 32, a.n, a.bs), a.n));
+  const WalkClasses wc = uniform_walk(walk_classes(row_group_bounds(train_row_group(qrow0, 32, a.n, a.bs), a.n),
+                                                   t0, n_first, t2, n_tiles - n_first, a.n, kSwRows, 0, kSwRows));
 
   f32x16 o[2] = {};  // O^T [d block]
   // mref: the row's reference maximum (log2 units); the score chains start
@@ -244,21 +242,10 @@ __global__ __launch_bounds__(256, OCC) void attn_fwd_dma_kernel(FwdArgs a) {
     const bool pf = it + kAhead < n_tiles;
     if (pf) issue(cur + kAhead < kStages ? cur + kAhead : cur + kAhead - kStages);
     const int k0 = wave_uniform(tile_of(it) * kSwRows);
-    // Classes of the two 32-key halves for this wave's rows; a tile is
-    // partial when either live half is.
-    const int c0 = bounds_class(cb, k0, 32, a.n);
-    const int c1 = bounds_class(cb, k0 + 32, 32, a.n);
-#if BD3_FWD_HALF
-    const int cls = (c0 == kPartial || c1 == kPartial) ? kPartial : kFull;
-    if (c0 != kNone && c1 != kNone)
-      step(std::integral_constant<int, 2>(), 0, k0, cls, smem[cur][0], smem[cur][1]);
-    else if ((c0 | c1) != kNone)
-      step(std::integral_constant<int, 1>(), c0 != kNone ? 0 : 1, k0, cls, smem[cur][0], smem[cur][1]);
-#else
-    const int cls = (c0 == kFull && c1 == kFull) ? kFull : kPartial;
-    if ((c0 | c1) != kNone)
-      step(std::integral_constant<int, 2>(), 0, k0, cls, smem[cur][0], smem[cur][1]);
-#endif
+    // The tile's class for this wave's rows.
+    if (walk_live(wc, it, n_first))
+      step(std::integral_constant<int, 2>(), 0, k0, walk_full(wc, it, n_first) ? kFull : kPartial, smem[cur][0],
+           smem[cur][1]);
     // Tile it+1 complete (the loads of later tiles may stay in flight), and
     // every wave is done reading stage `cur` before it is refilled.
     if (pf)

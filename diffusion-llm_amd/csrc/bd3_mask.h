@@ -272,6 +272,57 @@ BD3_HD int bounds_class(const ClassBounds& b, int p, int C, int n) {
   return live ? (full ? kFull : kPartial) : kNone;
 }
 
+// Floor and ceiling of a / b for b > 0 and any sign of a.
+BD3_HD int floor_div(int a, int b) { return a >= 0 ? a / b : -((b - 1 - a) / b); }
+BD3_HD int ceil_div(int a, int b) { return -floor_div(-a, b); }
+
+// The classes of the tiles of a walk for one fixed group, as intervals of the
+// walk index. The walk visits tiles t0 .. t0 + n_first - 1 (walk index
+// i = 0 .. n_first - 1), then t2 .. t2 + n_second - 1 (i = n_first ..); each
+// range lies in one half. The classified positions of tile t are
+// [t * tile + off, t * tile + off + C) (the whole tile, or one 32-wide half
+// of it). Tile i is live iff i - live_lo[r] < live_len[r] and full iff
+// i - full_lo[r] < full_len[r] (unsigned differences), r = 0 in the first
+// range and 1 in the second: the same classes as bounds_class(b, t * tile +
+// off, C, n), at a few scalar operations per tile.
+struct WalkClasses {
+  int live_lo[2], live_len[2], full_lo[2], full_len[2];
+};
+
+BD3_HD WalkClasses walk_classes(const ClassBounds& b, int t0, int n_first, int t2, int n_second, int n,
+                                int tile, int off, int C) {
+  WalkClasses w;
+  const int ta[2] = {t0, t2}, cnt[2] = {n_first, n_second};
+  int base = 0;
+  for (int r = 0; r < 2; ++r) {
+    const int h = ta[r] * tile + off >= n;
+    // p = t * tile + off: live iff p + C > lo and p < hi; full iff p >= flo
+    // and p + C <= fhi.
+    const int l0 = floor_div(b.lo[h] - off - C, tile) + 1, l1 = ceil_div(b.hi[h] - off, tile);
+    const int f0 = ceil_div(b.flo[h] - off, tile), f1 = floor_div(b.fhi[h] - off - C, tile) + 1;
+    // walk indices, clipped to the range; full tiles are live tiles
+    const int li0 = imin(imax(l0 - ta[r], 0), cnt[r]), li1 = imin(imax(l1 - ta[r], 0), cnt[r]);
+    const int fi0 = imax(imin(imax(f0 - ta[r], 0), cnt[r]), li0);
+    const int fi1 = imin(imin(imax(f1 - ta[r], 0), cnt[r]), li1);
+    w.live_lo[r] = base + li0;
+    w.live_len[r] = imax(li1 - li0, 0);
+    w.full_lo[r] = base + fi0;
+    w.full_len[r] = imax(fi1 - fi0, 0);
+    base += cnt[r];
+  }
+  return w;
+}
+
+// Whether walk tile i is live / full under w (scalar code for a uniform w).
+BD3_HD bool walk_live(const WalkClasses& w, int i, int n_first) {
+  const bool r0 = i < n_first;
+  return (unsigned)(i - (r0 ? w.live_lo[0] : w.live_lo[1])) < (unsigned)(r0 ? w.live_len[0] : w.live_len[1]);
+}
+BD3_HD bool walk_full(const WalkClasses& w, int i, int n_first) {
+  const bool r0 = i < n_first;
+  return (unsigned)(i - (r0 ? w.full_lo[0] : w.full_lo[1])) < (unsigned)(r0 ? w.full_len[0] : w.full_len[1]);
+}
+
 // Key ranges (in key-tile units of `tile` keys) a training row group
 // [q0, q0+R) must visit: up to two half-open tile ranges [t0, t1) and
 // [t2, t3). Rows must lie in one half. Every live pair of the group lies in

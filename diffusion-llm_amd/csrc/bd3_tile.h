@@ -23,6 +23,18 @@ __device__ __forceinline__ ClassBounds uniform_bounds(ClassBounds b) {
   return b;
 }
 
+// Walk-index class intervals moved to SGPRs.
+__device__ __forceinline__ WalkClasses uniform_walk(WalkClasses w) {
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    w.live_lo[r] = wave_uniform(w.live_lo[r]);
+    w.live_len[r] = wave_uniform(w.live_len[r]);
+    w.full_lo[r] = wave_uniform(w.full_lo[r]);
+    w.full_len[r] = wave_uniform(w.full_len[r]);
+  }
+  return w;
+}
+
 // Sum of the 8 bf16 values of a P operand added to acc, as 4 v_dot2c_f32_bf16
 // against (1, 1): the softmax denominator accumulates exactly the rounded
 // probabilities the PV product uses, at half the VALU cost of fp32 adds.

@@ -651,6 +651,29 @@ int bd3_train_classify_keys(int32_t n, int32_t block_size, int32_t q0, int32_t k
   return bd3::bounds_class(bd3::key_group_bounds(g, n), q0, 32, n) == c ? c : -2;
 }
 
+int bd3_train_walk_class(int32_t n, int32_t block_size, int32_t g0, int32_t i, int32_t mode, int32_t* tile) {
+  if (tile == nullptr || n < 128 || n % 128 != 0 || block_size < 1 || (mode != 0 && mode != 1)) return -1;
+  if (g0 < 0 || g0 + 32 > 2 * n || g0 % 32 || i < 0) return -1;
+  // mode 0: a 32-row group of a 128-row query tile walking key tiles (forward,
+  // dQ); mode 1: a 32-key group of a 128-key tile walking query tiles (dK/dV).
+  const bd3::KeyRanges kr = mode == 0 ? bd3::train_key_ranges(g0 - g0 % 128, 128, n, block_size, 64)
+                                      : bd3::train_query_ranges(g0 - g0 % 128, 128, n, block_size, 64);
+  const int n_first = kr.t1 - kr.t0, n_second = kr.t3 - kr.t2;
+  if (i >= n_first + n_second) return -3;
+  const bd3::ClassBounds b = mode == 0 ? bd3::row_group_bounds(bd3::train_row_group(g0, 32, n, block_size), n)
+                                       : bd3::key_group_bounds(bd3::train_key_group(g0, 32, n, block_size), n);
+  *tile = i < n_first ? kr.t0 + i : kr.t2 + (i - n_first);
+  int out = 0;
+  const int parts[3][2] = {{0, 64}, {0, 32}, {32, 32}};  // whole tile, first half, second half
+  for (int p = 0; p < 3; ++p) {
+    const bd3::WalkClasses w = bd3::walk_classes(b, kr.t0, n_first, kr.t2, n_second, n, 64, parts[p][0], parts[p][1]);
+    const int c = bd3::walk_live(w, i, n_first) ? (bd3::walk_full(w, i, n_first) ? bd3::kFull : bd3::kPartial)
+                                                : bd3::kNone;
+    out |= c << (2 * p);
+  }
+  return out;
+}
+
 int bd3_train_intervals(int32_t n, int32_t block_size, int32_t index, int32_t mode, int32_t* out) {
   if (out == nullptr || n < 1 || block_size < 1 || index < 0 || index >= 2 * n) return -1;
   if (mode != 0 && mode != 1) return -1;

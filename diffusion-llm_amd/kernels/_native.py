@@ -61,6 +61,7 @@ SIGNATURES: dict[str, tuple] = {
     "bd3_train_tile_census": (ctypes.c_int, [_i32, _i32, _i64p]),
     "bd3_train_classify": (ctypes.c_int, [_i32, _i32, _i32, _i32]),
     "bd3_train_classify_keys": (ctypes.c_int, [_i32, _i32, _i32, _i32]),
+    "bd3_train_walk_class": (ctypes.c_int, [_i32, _i32, _i32, _i32, _i32, ctypes.POINTER(ctypes.c_int32)]),
     "bd3_train_intervals": (ctypes.c_int, [_i32, _i32, _i32, _i32, ctypes.POINTER(ctypes.c_int32)]),
 }
 

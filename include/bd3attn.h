@@ -383,6 +383,20 @@ int bd3_train_classify_keys(int32_t n, int32_t block_size, int32_t q0,
                             int32_t k0);
 
 /*
+ * Host-only: tile classes (0 none, 1 full, 2 partial) in the walk-index
+ * interval form (walk_classes in the device headers). The forward kernel
+ * keeps these intervals in scalar registers and uses the whole-tile class
+ * of mode 0. mode 0: the 32-row group starting at g0, walking the key tiles
+ * (64 keys) of its 128-row query tile; mode 1: the 32-key group starting at
+ * g0, walking the query tiles (64 rows) of its 128-key tile. *tile receives
+ * the i-th tile's index. Returns the class of the whole tile | (class of its
+ * first 32 positions) << 2 | (class of its last 32) << 4; -1 on bad
+ * arguments, -3 when the walk has fewer than i + 1 tiles. For CPU tests.
+ */
+int bd3_train_walk_class(int32_t n, int32_t block_size, int32_t g0, int32_t i, int32_t mode,
+                         int32_t* tile);
+
+/*
  * Host-only: the interval form of the training mask the kernels apply inside
  * partial blocks, for CPU tests. mode 0: the keys row `index` sees; mode 1:
  * the rows that see key `index`. Writes out[0..3] = {lo1, hi1, lo2, hi2}:

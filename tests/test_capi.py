@@ -73,6 +73,48 @@ def test_classification_exact(lib, n, bs):
             assert lib.bd3_train_classify_keys(n, bs, q0, k0) == want, (q0, k0)
 
 
+def _cls(blk):
+    return 0 if not blk.any() else (1 if blk.all() else 2)
+
+
+@pytest.mark.parametrize("n,bs", [(128, 1), (128, 16), (128, 100), (256, 7), (256, 48), (384, 64),
+                                  (512, 512), (1024, 16), (640, 33)])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_walk_classes_match_mask(lib, n, bs, mode):
+    """Per-tile classes in walk-index interval form (the forward kernel's
+    whole-tile classes are mode 0) against the mask. mode 0: 32-row groups
+    walking the key tiles of their 128-row query tile; mode 1: 32-key groups
+    walking the query tiles of their 128-key tile. The walk visits
+    distinct tiles and every tile where the 128-wide tile has a live pair;
+    each tile of it is none / full / partial for the group exactly as the
+    group's 32 x 64 mask block is, and so is each 32 x 32 half."""
+    m = block_diff_mask(n, bs)
+    if mode == 1:
+        m = m.T  # rows <-> keys: a key group's view of the queries
+    tile = ctypes.c_int32()
+    for g0 in range(0, 2 * n, 32):
+        walk, classes = [], []
+        while True:
+            c = lib.bd3_train_walk_class(n, bs, g0, len(walk), mode, ctypes.byref(tile))
+            if c == -3:
+                break
+            assert c >= 0, (g0, c)
+            walk.append(tile.value)
+            classes.append(c)
+        assert len(set(walk)) == len(walk), (g0, walk)
+        r0 = g0 - g0 % 128
+        need = {t for t in range(2 * n // 64) if m[r0:r0 + 128, 64 * t:64 * t + 64].any()}
+        assert need <= set(walk), (g0, sorted(need - set(walk)))
+        for t, c in zip(walk, classes):
+            blk = m[g0:g0 + 32, 64 * t:64 * t + 64]
+            want = _cls(blk) | _cls(blk[:, :32]) << 2 | _cls(blk[:, 32:]) << 4
+            assert c == want, (g0, t, c, want)
+    assert lib.bd3_train_walk_class(n, bs, 0, 10 ** 6, mode, ctypes.byref(tile)) == -3
+    assert lib.bd3_train_walk_class(n, bs, 16, 0, mode, ctypes.byref(tile)) == -1
+    assert lib.bd3_train_walk_class(n, bs, 0, 0, mode, None) == -1
+    assert lib.bd3_train_walk_class(n, bs, 0, 0, 2, ctypes.byref(tile)) == -1
+
+
 @pytest.mark.parametrize("n,bs", [(8, 1), (8, 3), (64, 16), (96, 7), (128, 128), (256, 64)])
 def test_interval_forms_match_mask(lib, n, bs):
     """The row intervals (forward, dQ kernels) and column intervals (dK/dV
