@@ -24,7 +24,13 @@
 //   lane is spent on absent queries. Waves step over 32-key chunks fetched
 //   with full-row loads into registers, staged through wave-private LDS
 //   tiles; the loads of a wave's next chunk are in flight while the current
-//   one is computed.
+//   one is computed. When one workgroup per split would overfill the GPU, a
+//   workgroup takes several consecutive splits (splits_per_group): its waves
+//   deal the chunks of all of them out continuously and merge each split's
+//   share into their running state at the split's end (the same LSE merge
+//   the combine pass applies), so the result equals one partial per split
+//   merged, with fewer partials in memory (none when one workgroup covers
+//   all of a head's splits).
 // decode_combine: merges the splits, weights exp2(lse_s - max lse) (the
 //   reference's split_kv_reduce_kern arithmetic, :109-127), 4 outputs per
 //   thread.
@@ -380,8 +386,9 @@ __global__ __launch_bounds__(NW * 64, BD3_DEC16_OCC) void decode16_partial(Decod
     const int lo = split_lo(sp), hi = split_hi(sp);
     return hi > lo ? (hi - lo + kChunk16 - 1) / kChunk16 : 0;
   };
+  int crot = bh * 7;  // start rotation of the chunks inside a split (mod its chunk count)
   auto chunk_c0 = [&](int sp, int nc, int i) {
-    const int c = i + (nc > 0 ? (bh * 7) % nc : 0);
+    const int c = i + (nc > 0 ? crot % nc : 0);
     return split_lo(sp) + (c >= nc ? c - nc : c) * kChunk16;
   };
 
@@ -415,27 +422,39 @@ __global__ __launch_bounds__(NW * 64, BD3_DEC16_OCC) void decode16_partial(Decod
     // chunk of the next split) stream in while the current chunk is computed.
     // The workgroup's chunks, split after split, are dealt to the waves in
     // turn (chunk g of the sequence to wave g mod NW), so every wave gets the
-    // same count to within one whatever the chunks per split.
-    int sp = s0, nc = n_chunks_of(s0), i = wave;
-    while (sp < s1 && i >= nc) {
+    // same count to within one whatever the chunks per split. The head
+    // starts where the one-split order starts it, chunk 7 bh of its chunks
+    // (mod their count): the splits are visited from the one holding that
+    // chunk on (j-th visited: s0 + (j + rot) mod cnt) and each split's chunks
+    // from the same offset on, so heads read different parts of their caches
+    // at any moment (the merge is order-independent up to rounding).
+    const int cnt = s1 - s0;
+    const int ncf = wave_uniform(imax(a.split_len / kChunk16, 1));  // chunks of a full split
+    const int start = wave_uniform((bh * 7) % (cnt * ncf));
+    const int rot = wave_uniform(start / ncf);
+    crot = start - rot * ncf;
+    auto act = [&](int j) { return s0 + (j + rot >= cnt ? j + rot - cnt : j + rot); };
+    int vs = 0, nc = n_chunks_of(act(0)), i = wave;
+    while (vs < cnt && i >= nc) {
       i -= nc;
-      ++sp;
-      nc = sp < s1 ? n_chunks_of(sp) : 0;
+      ++vs;
+      nc = vs < cnt ? n_chunks_of(act(vs)) : 0;
     }
-    if (sp < s1) load(chunk_c0(sp, nc, i));
+    if (vs < cnt) load(chunk_c0(act(vs), nc, i));
     float ms = -INFINITY, ls = 0.f;
     f32x4 os[4] = {};
-    while (sp < s1) {
+    while (vs < cnt) {
       stage();
-      int sp_n = sp, nc_n = nc, i_n = i + NW;
-      while (sp_n < s1 && i_n >= nc_n) {
+      int vs_n = vs, nc_n = nc, i_n = i + NW;
+      while (vs_n < cnt && i_n >= nc_n) {
         i_n -= nc_n;
-        ++sp_n;
-        nc_n = sp_n < s1 ? n_chunks_of(sp_n) : 0;
+        ++vs_n;
+        nc_n = vs_n < cnt ? n_chunks_of(act(vs_n)) : 0;
       }
-      if (sp_n < s1) load(chunk_c0(sp_n, nc_n, i_n));
+      if (vs_n < cnt) load(chunk_c0(act(vs_n), nc_n, i_n));
+      const int sp = act(vs);
       chunk(chunk_c0(sp, nc, i), split_hi(sp), ms, ls, os);
-      if (sp_n != sp) {
+      if (vs_n != vs) {
         // the wave's share of split sp is done: merge its normalised partial
         float lrow = ls + shfl_xor(ls, 16);
         lrow = sum_xor32(lrow);
@@ -455,7 +474,7 @@ __global__ __launch_bounds__(NW * 64, BD3_DEC16_OCC) void decode16_partial(Decod
 #pragma unroll
         for (int db = 0; db < 4; ++db) os[db] = f32x4{};
       }
-      sp = sp_n;
+      vs = vs_n;
       nc = nc_n;
       i = i_n;
     }

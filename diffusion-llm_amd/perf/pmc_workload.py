@@ -15,7 +15,15 @@ Dispatches, in order and each `--reps` times:
      full 8 x 2048-token sequence, 12 heads;
   5. LayerNorm + adaLN modulate (bd3_ln_modulate) over 8 x 2048 tokens of
      d_model 768 (fp32 residual, bf16 vectors, bf16 result).
-No timing is done here; the profiler records per-dispatch counters.
+With --decode-b1 only (no calibration copy, training or other kernels): the
+reference's decode profiling shapes (bench/decode_ncu.py:16-19), batch 1,
+12 heads, block 16 - a 16-token block over a 3584-token cache and the whole
+3088-token sequence block-causal - each through bd3_decode (automatic split
+count) and the split_kv path (the reference rule ceil(kv_len / 256) for the
+cached shape; prefill falls back to the block-sparse path as the reference
+does, kernels/SplitKVDecodeAttention.py:140-147).
+No timing is done here; the profiler records per-dispatch counters (or, under
+--kernel-trace --stats, durations).
 """
 from __future__ import annotations
 
@@ -38,6 +46,7 @@ def main(argv=None) -> int:
     ap.add_argument("--seq-len", type=int, default=1024)
     ap.add_argument("--block-size", type=int, default=16)
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--decode-b1", action="store_true", help="only the batch-1 decode profiling shapes")
     args = ap.parse_args(argv)
 
     import torch
@@ -45,6 +54,8 @@ def main(argv=None) -> int:
     from kernels._native import check, lib, ptr, stream_of, strides
 
     dev = torch.device("cuda:0")
+    if args.decode_b1:
+        return decode_b1(args.reps, dev)
     n_el = args.copy_mib * (1 << 20) // 4
     src = torch.ones(n_el, device=dev, dtype=torch.float32)
     dst = torch.empty_like(src)
@@ -102,6 +113,24 @@ def main(argv=None) -> int:
         ln_modulate(x, w, sh, sh, out_dtype=torch.bfloat16)
     torch.cuda.synchronize()
     print(f"ln_modulate done (x bytes read per dispatch {x.numel() * 4})", flush=True)
+    return 0
+
+
+def decode_b1(reps: int, dev) -> int:
+    import torch
+    from bench import seeded_bf16
+    from kernels.BlockSparseDecodeAttention import block_sparse_decode_attention
+    from kernels.SplitKVDecodeAttention import split_kv_decode_attention
+    D = 64
+    for shape, (q_len, kv_len) in (("cached", (16, 3584)), ("uncached", (3088, 3088))):
+        (q,) = seeded_bf16((1, 12, q_len, D), 3, 1, dev)
+        k, v = seeded_bf16((1, 12, kv_len, D), 4, 2, dev)
+        for name, fn in (("bsdfa", block_sparse_decode_attention), ("split_kv", split_kv_decode_attention)):
+            for _ in range(reps):
+                fn(q, k, v, 16)
+            torch.cuda.synchronize()
+            print(f"decode batch 1 {shape} ({q_len} over {kv_len}) via {name}: {reps} calls", flush=True)
+        del q, k, v
     return 0
 
 
