@@ -181,16 +181,17 @@ def time_train(step: TrainStep, steps: int, warmup: int, use_graph: bool = False
     (bench/attention_bench.py:61-76 with bench/harness.py:25-51): the caches
     are evicted (a 1 GiB read, larger than the 256 MB Infinity Cache) before
     the forward and again before the backward, and HIP events on the launch
-    stream time each; fwd+bwd is their sum. Events also separate the
+    stream (fence-free, perf.harness.StreamEvent) time each; fwd+bwd is their
+    sum. Events also separate the
     backward's two kernels (dQ, dK/dV). With `use_graph` the forward and the
     backward are replayed from two captured HIP graphs. The same steps are
     also timed back to back without eviction (wall clock) for comparison.
 
     Returns a dict: step_ms (median, p20, p80, mean of fwd + bwd over the
-    timed steps), kernel_ms (median of each kernel), warm_ms_per_step,
-    launch."""
+    timed steps), kernel_ms / kernel_mean_ms (median / mean of each kernel),
+    warm_ms_per_step, launch."""
     import torch
-    from perf.harness import Samples, flush_caches
+    from perf.harness import Samples, StreamEvent, flush_caches
     # Ramp: on a freshly started process the step runs ~15% slow for the
     # first ~1.5 s of load (clocks and first touches settling), far longer
     # than W warm-up steps last.
@@ -210,7 +211,7 @@ def time_train(step: TrainStep, steps: int, warmup: int, use_graph: bool = False
     events = []
     torch.cuda.synchronize()
     for _ in range(steps):
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
+        ev = [StreamEvent() for _ in range(5)]
         flush_caches()
         ev[0].record(stream)
         fwd_fn()
@@ -228,11 +229,12 @@ def time_train(step: TrainStep, steps: int, warmup: int, use_graph: bool = False
         events.append(ev)
     torch.cuda.synchronize()
     total = Samples([e[0].elapsed_time(e[1]) + e[2].elapsed_time(e[4]) for e in events])
-    kernel_ms = {"fwd": Samples([e[0].elapsed_time(e[1]) for e in events]).median_ms,
-                 "bwd": Samples([e[2].elapsed_time(e[4]) for e in events]).median_ms}
+    spans = {"fwd": (0, 1), "bwd": (2, 4)}
     if graphs is None:
-        kernel_ms["bwd_dq"] = Samples([e[2].elapsed_time(e[3]) for e in events]).median_ms
-        kernel_ms["bwd_dkdv"] = Samples([e[3].elapsed_time(e[4]) for e in events]).median_ms
+        spans.update(bwd_dq=(2, 3), bwd_dkdv=(3, 4))
+    per = {k: Samples([e[a].elapsed_time(e[b]) for e in events]) for k, (a, b) in spans.items()}
+    kernel_ms = {k: v.median_ms for k, v in per.items()}
+    kernel_mean_ms = {k: v.mean_ms for k, v in per.items()}
     # the same steps back to back, caches warm, wall clock
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -243,7 +245,7 @@ def time_train(step: TrainStep, steps: int, warmup: int, use_graph: bool = False
     warm = (time.perf_counter() - t0) * 1e3 / steps
     return {"step_ms": {"median": total.median_ms, "p20": total.p20_ms, "p80": total.p80_ms,
                         "mean": total.mean_ms},
-            "kernel_ms": kernel_ms, "warm_ms_per_step": warm,
+            "kernel_ms": kernel_ms, "kernel_mean_ms": kernel_mean_ms, "warm_ms_per_step": warm,
             "launch": "hip_graph" if graphs is not None else "eager"}
 
 
@@ -623,7 +625,7 @@ def train_record(step: "TrainStep", t: dict) -> dict:
     fwd = useful_fwd_flops(B, H, n, bs)
     ms = t["step_ms"]["median"]
     rec = {"ms_per_step": ms, "step_ms": t["step_ms"], "warm_ms_per_step": t["warm_ms_per_step"],
-           "launch": t["launch"], "kernel_ms": t["kernel_ms"],
+           "launch": t["launch"], "kernel_ms": t["kernel_ms"], "kernel_mean_ms": t["kernel_mean_ms"],
            "useful_tflops": 3.5 * fwd / (ms * 1e-3) / 1e12,
            "frac_of_peak": 3.5 * fwd / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
            "census": census(n, bs)}
@@ -714,7 +716,7 @@ def main(argv=None) -> int:
     # Dominant kernel's roofline: its algorithmic (useful) FLOPs per launch,
     # the FA2 credit of the products it owns (forward 1x the useful forward
     # FLOPs; dQ kernel 0.5x: the dQ product; dK/dV kernel 2x: S, dP, dV, dK),
-    # over its median launch duration inside the timed steps.
+    # over its average (mean) launch duration inside the timed steps.
     fwd_flops = useful_fwd_flops(B, H, n, bs)
     credit = {"fwd": 1.0, "bwd_dq": 0.5, "bwd_dkdv": 2.0}
     names = {"fwd": "attn_fwd_dma_kernel", "bwd_dq": "attn_bwd_dq_dma_kernel",
@@ -722,7 +724,8 @@ def main(argv=None) -> int:
     per = {k: v for k, v in per.items() if k in credit}
     dom = max(per, key=per.get) if per else "bwd_dkdv"
     dom_flops = credit[dom] * fwd_flops
-    achieved = dom_flops / (per[dom] * 1e-3) / 1e12 if per else None
+    dom_mean = t["kernel_mean_ms"].get(dom)
+    achieved = dom_flops / (dom_mean * 1e-3) / 1e12 if dom_mean else None
 
     result = {
         "metric": metric,
@@ -745,6 +748,7 @@ def main(argv=None) -> int:
                      "frac": achieved / PEAK_BF16_TFLOPS if achieved else None,
                      "traffic": measured_traffic(names[dom]),
                      "kernel": names[dom], "algorithmic_flops_per_launch": dom_flops,
+                     "mean_launch_us": dom_mean * 1e3 if dom_mean else None,
                      "credit": f"{credit[dom]} x useful forward FLOPs (FA2 convention: backward = 2.5x forward, "
                                "dQ kernel owns the dQ product, dK/dV kernel S, dP, dV, dK)"},
     }

@@ -1,6 +1,13 @@
 """Device timing for the benchmarks: per-call HIP-event samples taken on the
 launch stream, each call preceded by an eviction of the GPU caches.
 
+The events are created with hipEventDisableSystemFence (`StreamEvent`). A
+default HIP timing event writes back and invalidates the GPU caches when it
+is recorded; on MI355X that adds several microseconds to every timed interval
+(measured: the three training kernels' event times exceed their rocprofv3
+kernel durations by 5-6 us each) and empties the caches the next kernel
+would have found warm. The fence-free event only stamps the time.
+
 The reference times its kernels with CUDA events after clearing a 256 MiB
 buffer (bench/harness.py:25-51). On MI355X that does not empty the caches a
 kernel's inputs may sit in: 4 MB of L2 per XCD plus the 256 MB Infinity
@@ -14,6 +21,7 @@ with the timed call for HBM.
 """
 from __future__ import annotations
 
+import ctypes
 import statistics
 import time
 from collections.abc import Callable, Sequence
@@ -22,6 +30,58 @@ from typing import Any
 import torch
 
 EVICT_BYTES = 1 << 30
+HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000  # hip_runtime_api.h
+
+_hip: ctypes.CDLL | None = None
+
+
+def _hip_runtime() -> ctypes.CDLL:
+    """The HIP runtime torch has loaded (found by its soname), with the
+    event entry points typed."""
+    global _hip
+    if _hip is None:
+        torch.cuda.init()
+        h = ctypes.CDLL("libamdhip64.so.7")
+        vp, p = ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)
+        h.hipEventCreateWithFlags.argtypes = [p, ctypes.c_uint]
+        h.hipEventRecord.argtypes = [vp, vp]
+        h.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), vp, vp]
+        h.hipEventDestroy.argtypes = [vp]
+        for f in (h.hipEventCreateWithFlags, h.hipEventRecord, h.hipEventElapsedTime, h.hipEventDestroy):
+            f.restype = ctypes.c_int
+        _hip = h
+    return _hip
+
+
+class StreamEvent:
+    """A HIP timing event without the system-scope fence (see the module
+    docstring), recorded on a torch stream."""
+
+    def __init__(self):
+        self._h = _hip_runtime()
+        self._ev = ctypes.c_void_p()
+        st = self._h.hipEventCreateWithFlags(ctypes.byref(self._ev), HIP_EVENT_DISABLE_SYSTEM_FENCE)
+        if st != 0:
+            raise RuntimeError(f"hipEventCreateWithFlags failed: {st}")
+
+    def record(self, stream: torch.cuda.Stream | None = None) -> None:
+        stream = stream or torch.cuda.current_stream()
+        st = self._h.hipEventRecord(self._ev, ctypes.c_void_p(stream.cuda_stream))
+        if st != 0:
+            raise RuntimeError(f"hipEventRecord failed: {st}")
+
+    def elapsed_time(self, end: "StreamEvent") -> float:
+        """Milliseconds from this event to `end` (both must have completed)."""
+        ms = ctypes.c_float()
+        st = self._h.hipEventElapsedTime(ctypes.byref(ms), self._ev, end._ev)
+        if st != 0:
+            raise RuntimeError(f"hipEventElapsedTime failed: {st}")
+        return ms.value
+
+    def __del__(self):
+        if getattr(self, "_ev", None) and self._ev.value:
+            self._h.hipEventDestroy(self._ev)
+            self._ev = ctypes.c_void_p()
 
 
 class CacheEvictor:
@@ -86,7 +146,7 @@ class Samples:
 def time_calls(fn: Callable[[], Any], reps: int = 30, warmup: int = 5, flush: bool = True,
                stream: torch.cuda.Stream | None = None) -> Samples:
     """Run fn() `warmup` times untimed, then `reps` times, each timed by a
-    pair of HIP events recorded on `stream` (default: the current stream,
+    pair of StreamEvents recorded on `stream` (default: the current stream,
     which is where the library's wrappers launch). With `flush`, the caches
     are evicted before every timed call, outside the events. Without a GPU
     the host clock times each call instead."""
@@ -105,7 +165,7 @@ def time_calls(fn: Callable[[], Any], reps: int = 30, warmup: int = 5, flush: bo
     for _ in range(reps):
         if flush:
             flush_caches()
-        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start, stop = StreamEvent(), StreamEvent()
         start.record(stream)
         fn()
         stop.record(stream)
