@@ -41,7 +41,15 @@ def _hip_runtime() -> ctypes.CDLL:
     global _hip
     if _hip is None:
         torch.cuda.init()
-        h = ctypes.CDLL("libamdhip64.so.7")
+        h = None
+        for soname in ("libamdhip64.so.7", "libamdhip64.so"):
+            try:
+                h = ctypes.CDLL(soname)
+                break
+            except OSError:
+                continue
+        if h is None:
+            raise RuntimeError("the HIP runtime (libamdhip64) is not loadable")
         vp, p = ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)
         h.hipEventCreateWithFlags.argtypes = [p, ctypes.c_uint]
         h.hipEventRecord.argtypes = [vp, vp]
