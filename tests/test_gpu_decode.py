@@ -49,6 +49,31 @@ def test_splitkv_matches_oracle(cuda, B, H, q_len, kv_len, bs, n_splits):
     assert max_abs(o, ref) <= OUT_TOL
 
 
+# Shapes where one workgroup takes several consecutive splits (batch * heads * n_splits > 512 and
+# at least 4 splits per workgroup): ragged key counts, short or empty last splits, q_len 1..16,
+# block sizes off the 16-key strips.
+GROUPED = [(4, 12, 16, 1000, 16, 33), (8, 12, 7, 3001, 5, 20), (2, 16, 16, 4112, 16, 64),
+           (16, 12, 1, 777, 16, 12), (8, 8, 16, 2048, 64, 40), (3, 12, 11, 1234, 3, 30)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,H,q_len,kv_len,bs,n_splits", GROUPED)
+def test_grouped_splits_match_oracle(cuda, record_error, B, H, q_len, kv_len, bs, n_splits):
+    """decode16_partial with several splits per workgroup (each wave's share of
+    a split merged on chip, heads starting at rotated splits) against the
+    oracle and against one split."""
+    q, k, v = decode_inputs(B, H, q_len, kv_len, seed=B * 1000 + kv_len + n_splits)
+    qd, kd, vd = (t.to(cuda, torch.bfloat16) for t in (q, k, v))
+    o = splitkv_capi(qd, kd, vd, bs, n_splits)
+    o1 = splitkv_capi(qd, kd, vd, bs, 1)
+    ref = decode_attention(q, k, v, bs)
+    torch.cuda.synchronize()
+    err = max_abs(o, ref)
+    record_error("decode O max-abs", err, OUT_TOL)
+    assert err <= OUT_TOL
+    assert max_abs(o, o1) <= 1e-2
+
+
 @pytest.mark.gpu
 def test_config3_split_invariance(cuda):
     """32 sequences x 12 heads, 16 queries over a
