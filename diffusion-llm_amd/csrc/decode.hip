@@ -537,7 +537,7 @@ __global__ __launch_bounds__(NW * 64, BD3_DEC16_OCC) void decode16_partial(Decod
 }
 
 // Split merge: thread -> (row, 4 consecutive d); rows in passes of 16. For
-// NS > 0 the call has exactly NS splits and all 2 NS loads of a row are issued
+// NS > 0 the call has at most NS splits and all loads of a row are issued
 // before the first use (one memory round trip); NS == 0 takes any count.
 template <int NS>
 __global__ __launch_bounds__(kThreads) void decode_combine(DecodeArgs a) {
@@ -557,18 +557,24 @@ __global__ __launch_bounds__(kThreads) void decode_combine(DecodeArgs a) {
     float mm = -INFINITY, wt = 0.f;
     f32x4 acc = {};
     if constexpr (NS > 0) {
+      const int ns = a.groups;  // <= NS
       float l[NS];
       f32x4 po[NS];
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
-        l[s] = lp[s * kQT];
-        po[s] = *reinterpret_cast<const f32x4*>(pp + s * kQT * kHeadDim);
+        if (s < ns) {
+          l[s] = lp[s * kQT];
+          po[s] = *reinterpret_cast<const f32x4*>(pp + s * kQT * kHeadDim);
+        } else {
+          l[s] = -INFINITY;
+          po[s] = f32x4{};
+        }
       }
 #pragma unroll
       for (int s = 0; s < NS; ++s) mm = fmaxf(mm, l[s]);
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
-        const float w = fast_exp2(l[s] - mm);  // empty split -> 0
+        const float w = s < ns ? fast_exp2(l[s] - mm) : 0.f;  // empty split -> 0
         wt += w;
         acc += w * po[s];
       }
@@ -636,12 +642,18 @@ hipError_t launch_decode(const DecodeArgs& a, int /*qt*/, hipStream_t stream) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.groups == 1) return e;
   const dim3 cgrid(a.q_tiles, a.bh);
-  switch (a.groups) {
-    case 2: hipLaunchKernelGGL(decode_combine<2>, cgrid, dim3(kThreads), 0, stream, a); break;
-    case 3: hipLaunchKernelGGL(decode_combine<3>, cgrid, dim3(kThreads), 0, stream, a); break;
-    case 4: hipLaunchKernelGGL(decode_combine<4>, cgrid, dim3(kThreads), 0, stream, a); break;
-    default: hipLaunchKernelGGL(decode_combine<0>, cgrid, dim3(kThreads), 0, stream, a); break;
-  }
+  if (a.groups == 2)
+    hipLaunchKernelGGL(decode_combine<2>, cgrid, dim3(kThreads), 0, stream, a);
+  else if (a.groups == 3)
+    hipLaunchKernelGGL(decode_combine<3>, cgrid, dim3(kThreads), 0, stream, a);
+  else if (a.groups == 4)
+    hipLaunchKernelGGL(decode_combine<4>, cgrid, dim3(kThreads), 0, stream, a);
+  else if (a.groups <= 16)
+    hipLaunchKernelGGL(decode_combine<16>, cgrid, dim3(kThreads), 0, stream, a);
+  else if (a.groups <= 32)
+    hipLaunchKernelGGL(decode_combine<32>, cgrid, dim3(kThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL(decode_combine<0>, cgrid, dim3(kThreads), 0, stream, a);
   return hipGetLastError();
 }
 

@@ -227,6 +227,9 @@ def test_workspace_sizes(lib):
     assert s == 1  # 384 workgroups at one split already cover 256 CUs
     # 96 (b, h) x 1 query tile: enough splits for 256 workgroups, at least 512 keys each
     assert [lib.bd3_decode_auto_splits(8, 12, 32, kv) for kv in (100, 544, 1056, 2080, 4096)] == [1, 1, 2, 3, 3]
+    # a cached step (q_len <= 16): down to 128 keys per split, at most 16 splits
+    assert [lib.bd3_decode_auto_splits(1, 12, 16, kv) for kv in (200, 544, 3584, 8192)] == [1, 4, 16, 16]
+    assert lib.bd3_decode_auto_splits(2, 12, 16, 1024) == 8
     assert lib.bd3_decode_workspace_bytes(32, 12, 16, 4112, 64, 0) == lib.bd3_decode_workspace_bytes(
         32, 12, 16, 4112, 64, s)
 
