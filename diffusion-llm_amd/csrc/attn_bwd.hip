@@ -52,7 +52,7 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dkdv_dma_kernel(BwdArgs a) 
   constexpr int kStageBytes = 4 * kSwTile + 1024;
   __shared__ __attribute__((aligned(1024))) __bf16 smem[kStages * kStageBytes / 2];
 
-  const int tid = threadIdx.x;
+  const int tid = wi_x();
   const int lane = tid & 63;
   const int wave = wave_uniform(tid >> 6);
   const int l32 = lane & 31;
@@ -286,13 +286,16 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dq_dma_kernel(BwdArgs a) {
   constexpr int kStages = 3;
   __shared__ __attribute__((aligned(1024))) __bf16 smem[kStages][2][kSwTile];  // [stage][K|V]
 
+  // threadIdx / blockIdx here, unlike the other kernels: with the id
+  // builtins the allocator spills one more VGPR in this kernel's tile loop
+  // (2 us slower at configs[1], outputs identical).
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = wave_uniform(tid >> 6);
   const int l32 = lane & 31;
   const int g = lane >> 5;
 
-  const BlockOrder bo(a.bh, a.heads);
+  const BlockOrder bo((int)blockIdx.x, a.bh, a.heads);
   const int tiles_half = a.n / kBM;
   const int t = tiles_half - 1 - (bo.rank >> 1);
   const int q0 = ((bo.rank & 1) ? 0 : a.n) + t * kBM;

@@ -28,6 +28,19 @@
 // is updated lazily: O and l are rescaled only when some row's max grew by
 // more than kRescale (log2 units); otherwise the stale max is kept, which
 // bounds P by 2^kRescale and leaves O / l exact.
+//
+// Prefill mode (prefill_attn_kernel, DecodeArgs): the same body over the
+// decode mask when many queries attend to the cache at once (the uncached
+// block-causal prefill of kernels/BlockSparseDecodeAttention.py:40-110 with
+// q_len = kv_len, or a long query block over a cached prefix). Row i of the
+// q_len queries sees keys [0, e(i)), e(i) = min(kv_len, (p / bs + 1) * bs),
+// p = kv_len - q_len + i: one interval per row, so a wave's tile classes
+// come from e at its first and last row. Work items are (128-row query
+// tile, split of the keys, batch*head), longest rows first; a query tile
+// whose keys all lie in the first split writes O, the others write
+// normalised fp32 partials and base-2 LSEs in the decode kernels' layout for
+// prefill_combine. Rows past q_len re-read the last query row and are not
+// stored; key rows past kv_len re-read the last key row and are masked.
 #include <type_traits>
 
 #include "bd3_device.h"
@@ -50,52 +63,85 @@ constexpr float kRescale = 8.0f;
 
 // One class per 64-key tile for the wave (dead / full / partial, as walk
 // index intervals of its row group): a full tile runs straight-line code with
-// no mask arithmetic. MASK16: the block size is a multiple of 16.
-template <int OCC, bool MASK16>
-__global__ __launch_bounds__(256, OCC) void attn_fwd_dma_kernel(FwdArgs a) {
+// no mask arithmetic. MASK16: every row's key intervals start and end on
+// multiples of 16 (training: the block size is a multiple of 16; prefill:
+// the block size and kv_len are).
+template <bool MASK16, bool PREFILL, class Args>
+__device__ __forceinline__ void fwd_body(Args a) {
   constexpr int kBM = 128;  // query rows per workgroup: 4 waves x 32
   constexpr int kStages = BD3_FWD_STAGES;
   constexpr int kAhead = kStages - 1;  // tiles requested ahead of the one being computed
   __shared__ __attribute__((aligned(1024))) __bf16 smem[kStages][2][kSwTile];  // [stage][K|V]
 
-  const int tid = threadIdx.x;
+  const int tid = wi_x();
   const int lane = tid & 63;
   const int wave = wave_uniform(tid >> 6);
   const int l32 = lane & 31;
   const int g = lane >> 5;
 
-  const BlockOrder bo(a.bh, a.heads);
-  const int tiles_half = a.n / kBM;
-  const int t = tiles_half - 1 - (bo.rank >> 1);
-  const int q0 = ((bo.rank & 1) ? 0 : a.n) + t * kBM;
+  int bh, b, h, q0;
+  int split = 0, e_wg = 0;  // prefill: the item's split and the tile's key end
+  if constexpr (PREFILL) {
+    bh = wg_x();
+    split = wg_y();
+    q0 = kBM * ((a.q_len + kBM - 1) / kBM - 1 - wg_z());
+    e_wg = decode_key_end(q0, kBM, a.q_len, a.kv_len, a.bs);
+    if (split * a.split_len >= e_wg) return;  // no key of this split is visible to the tile
+    b = bh / a.heads;
+    h = bh - b * a.heads;
+  } else {
+    const BlockOrder bo(a.bh, a.heads);
+    const int tiles_half = a.n / kBM;
+    const int t = tiles_half - 1 - (bo.rank >> 1);
+    q0 = ((bo.rank & 1) ? 0 : a.n) + t * kBM;
+    bh = bo.bh;
+    b = bo.b;
+    h = bo.h;
+  }
 
-  const uint16_t* qp = a.q + bo.b * a.sq.b + bo.h * a.sq.h;
-  const uint16_t* kp = uniform_ptr(a.k + bo.b * a.sk.b + bo.h * a.sk.h);
-  const uint16_t* vp = uniform_ptr(a.v + bo.b * a.sv.b + bo.h * a.sv.h);
+  const uint16_t* qp = a.q + b * a.sq.b + h * a.sq.h;
+  const uint16_t* kp = uniform_ptr(a.k + b * a.sk.b + h * a.sk.h);
+  const uint16_t* vp = uniform_ptr(a.v + b * a.sv.b + h * a.sv.h);
 
   const int qrow0 = q0 + 32 * wave;
   const int myq = qrow0 + l32;
+  int qsrc = myq;  // the row whose Q the lane holds
+  if constexpr (PREFILL) qsrc = imin(myq, a.q_len - 1);
   bf16x8 qreg[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c)
-    qreg[c] = __builtin_bit_cast(bf16x8, ld16(qp + (int64_t)myq * a.sq.s + 16 * c + 8 * g));
+    qreg[c] = __builtin_bit_cast(bf16x8, ld16(qp + (int64_t)qsrc * a.sq.s + 16 * c + 8 * g));
 
-  const KeyRanges kr = train_key_ranges(q0, kBM, a.n, a.bs, kSwRows);
-  const int t0 = wave_uniform(kr.t0), t2 = wave_uniform(kr.t2);
-  const int n_first = wave_uniform(kr.t1 - kr.t0);
-  const int n_tiles = n_first + wave_uniform(kr.t3 - kr.t2);
+  int t0, t2, n_first, n_tiles;
+  if constexpr (PREFILL) {
+    // One range: the split's tiles up to the tile's key end.
+    t0 = wave_uniform(split * (a.split_len / kSwRows));
+    const int kend = imin(e_wg, (split + 1) * a.split_len);
+    n_first = wave_uniform((kend + kSwRows - 1) / kSwRows - t0);
+    t2 = t0 + n_first;
+    n_tiles = n_first;
+  } else {
+    const KeyRanges kr = train_key_ranges(q0, kBM, a.n, a.bs, kSwRows);
+    t0 = wave_uniform(kr.t0);
+    t2 = wave_uniform(kr.t2);
+    n_first = wave_uniform(kr.t1 - kr.t0);
+    n_tiles = n_first + wave_uniform(kr.t3 - kr.t2);
+  }
   auto tile_of = [&](int i) { return i < n_first ? t0 + i : t2 + (i - n_first); };
 
   // Wave w fills the 1 KB blocks 2w and 2w+1 (rows 16w .. 16w+15) of each K
   // and V tile: lane L fetches logical chunk (L%8) ^ swz(row) of row
   // 16w + 8j + L/8 (byte offsets from the tile's row 0).
   uint32_t koff[2], voff[2];
+  int lrow[2], lch[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int r = 16 * wave + 8 * j + (lane >> 3);
     const int ch = 8 * ((lane & 7) ^ swz(r));
     koff[j] = (uint32_t)(2 * (r * (int)a.sk.s + ch));
     voff[j] = (uint32_t)(2 * (r * (int)a.sv.s + ch));
+    lrow[j] = r;
+    lch[j] = ch;
   }
   const int64_t kstep = (int64_t)kSwRows * a.sk.s, vstep = (int64_t)kSwRows * a.sv.s;
   // LDS byte address of this wave's first K block in stage 0; a stage is
@@ -107,10 +153,21 @@ __global__ __launch_bounds__(256, OCC) void attn_fwd_dma_kernel(FwdArgs a) {
   TilePtr kn(kp, 2 * kstep, t0, n_first, t2), vn(vp, 2 * vstep, t0, n_first, t2);
   auto issue = [&](int stage) {
     const uint32_t dst = lds_w + (uint32_t)stage * 16384u;
+    uint32_t ko[2] = {koff[0], koff[1]}, vo[2] = {voff[0], voff[1]};
+    if constexpr (PREFILL) {
+      // Rows past the last key re-read the last key row (masked out).
+      const int lim = a.kv_len - 1 - walk.tile * kSwRows;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) dma16(kn.cur, koff[j], dst + 1024u * j);
+      for (int j = 0; j < 2; ++j) {
+        const int r = imin(lrow[j], lim);
+        ko[j] = (uint32_t)(2 * (r * (int)a.sk.s + lch[j]));
+        vo[j] = (uint32_t)(2 * (r * (int)a.sv.s + lch[j]));
+      }
+    }
 #pragma unroll
-    for (int j = 0; j < 2; ++j) dma16(vn.cur, voff[j], dst + 8192u + 1024u * j);
+    for (int j = 0; j < 2; ++j) dma16(kn.cur, ko[j], dst + 1024u * j);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) dma16(vn.cur, vo[j], dst + 8192u + 1024u * j);
     const bool jumping = walk.left == 1;
     walk.next();
     kn.next(jumping);
@@ -128,9 +185,30 @@ __global__ __launch_bounds__(256, OCC) void attn_fwd_dma_kernel(FwdArgs a) {
   // exponent, and a chain started from -m gives S * scale * log2(e) - m.
 #pragma unroll
   for (int c = 0; c < 4; ++c) qreg[c] = scale_bf16x8(qreg[c], a.scale_log2);
-  const RowIntervals riv = train_row_intervals(myq, a.n, a.bs);
-  const WalkClasses wc = uniform_walk(walk_classes(row_group_bounds(train_row_group(qrow0, 32, a.n, a.bs), a.n),
-                                                   t0, n_first, t2, n_tiles - n_first, a.n, kSwRows, 0, kSwRows));
+  RowIntervals riv;
+  WalkClasses wc;
+  if constexpr (PREFILL) {
+    const int ql = a.q_len;
+    auto key_end = [&](int i) { return imin(((a.kv_len - ql + i) / a.bs + 1) * a.bs, a.kv_len); };
+    riv = RowIntervals{0, key_end(qsrc), 0, 0};
+    // Tiles below the first row's key end are full, those from the last
+    // row's key end on are dead; a wave with no row below q_len has none live.
+    ClassBounds cb;
+    const int emax = qrow0 < ql ? key_end(imin(qrow0 + 31, ql - 1)) : 0;
+    const int emin = key_end(imin(qrow0, ql - 1));
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      cb.lo[hh] = 0;
+      cb.hi[hh] = emax;
+      cb.flo[hh] = 0;
+      cb.fhi[hh] = emin;
+    }
+    wc = uniform_walk(walk_classes(cb, t0, n_first, t2, 0, kBoundBig, kSwRows, 0, kSwRows));
+  } else {
+    riv = train_row_intervals(myq, a.n, a.bs);
+    wc = uniform_walk(walk_classes(row_group_bounds(train_row_group(qrow0, 32, a.n, a.bs), a.n), t0, n_first, t2,
+                                   n_tiles - n_first, a.n, kSwRows, 0, kSwRows));
+  }
 
   f32x16 o[2] = {};  // O^T [d block]
   // mref: the row's reference maximum (log2 units); the score chains start
@@ -256,16 +334,111 @@ __global__ __launch_bounds__(256, OCC) void attn_fwd_dma_kernel(FwdArgs a) {
   }
 
   const float ltot = sum_xor32(lsum);
-  const float inv = 1.f / ltot;
-  uint16_t* op = a.o + bo.b * a.so.b + bo.h * a.so.h + (int64_t)myq * a.so.s;
+  if constexpr (PREFILL) {
+    if (myq >= a.q_len) return;
+    // A row may see no key of a later split: O = 0, LSE = -inf.
+    const bool seen = ltot > 0.f;
+    const float inv = seen ? 1.f / ltot : 0.f;
+    if (e_wg <= a.split_len) {  // the tile's keys all lie in the first split
+      uint16_t* op = a.o + b * a.so.b + h * a.so.h + (int64_t)myq * a.so.s;
 #pragma unroll
-  for (int db = 0; db < 2; ++db)
+      for (int db = 0; db < 2; ++db)
 #pragma unroll
-    for (int rg4 = 0; rg4 < 4; ++rg4)
-      *reinterpret_cast<bf16x4*>(op + 32 * db + 8 * rg4 + 4 * g) =
-          to_bf16x4(o[db][4 * rg4] * inv, o[db][4 * rg4 + 1] * inv, o[db][4 * rg4 + 2] * inv,
-                    o[db][4 * rg4 + 3] * inv);
-  if (g == 0) a.lse[(int64_t)bo.bh * 2 * a.n + myq] = (mref + fast_log2(ltot)) * kLn2;
+        for (int rg4 = 0; rg4 < 4; ++rg4)
+          *reinterpret_cast<bf16x4*>(op + 32 * db + 8 * rg4 + 4 * g) =
+              to_bf16x4(o[db][4 * rg4] * inv, o[db][4 * rg4 + 1] * inv, o[db][4 * rg4 + 2] * inv,
+                        o[db][4 * rg4 + 3] * inv);
+    } else {
+      const int64_t slot = ((int64_t)bh * a.q_tiles + (qrow0 >> 5)) * a.n_splits + split;
+      float* po = a.part_o + (slot * 32 + l32) * kHeadDim;
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int rg4 = 0; rg4 < 4; ++rg4)
+          *reinterpret_cast<f32x4*>(po + 32 * db + 8 * rg4 + 4 * g) =
+              f32x4{o[db][4 * rg4] * inv, o[db][4 * rg4 + 1] * inv, o[db][4 * rg4 + 2] * inv,
+                    o[db][4 * rg4 + 3] * inv};
+      if (g == 0) a.part_lse[slot * 32 + l32] = seen ? mref + fast_log2(ltot) : -INFINITY;
+    }
+  } else {
+    const float inv = 1.f / ltot;
+    uint16_t* op = a.o + b * a.so.b + h * a.so.h + (int64_t)myq * a.so.s;
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int rg4 = 0; rg4 < 4; ++rg4)
+        *reinterpret_cast<bf16x4*>(op + 32 * db + 8 * rg4 + 4 * g) =
+            to_bf16x4(o[db][4 * rg4] * inv, o[db][4 * rg4 + 1] * inv, o[db][4 * rg4 + 2] * inv,
+                      o[db][4 * rg4 + 3] * inv);
+    if (g == 0) a.lse[(int64_t)bh * 2 * a.n + myq] = (mref + fast_log2(ltot)) * kLn2;
+  }
+}
+
+template <int OCC, bool MASK16>
+__global__ __launch_bounds__(256, OCC) void attn_fwd_dma_kernel(FwdArgs a) {
+  fwd_body<MASK16, false>(a);
+}
+
+template <int OCC, bool MASK16>
+__global__ __launch_bounds__(256, OCC) void prefill_attn_kernel(DecodeArgs a) {
+  fwd_body<MASK16, true>(a);
+}
+
+// Merges the split partials of the rows whose 128-row tile spans several
+// splits (the kernel wrote the other rows' O): weights exp2(lse_s - max lse)
+// as in decode_combine, 16 threads per row, 4 outputs each, up to 8 splits
+// per memory round trip. Grid: (32-row tiles, batch*head).
+__global__ __launch_bounds__(256) void prefill_combine(DecodeArgs a) {
+  const int qt = wg_x();
+  const int bh = wg_y();
+  const int i0 = qt * 32;
+  const int e = decode_key_end(i0 & ~127, 128, a.q_len, a.kv_len, a.bs);
+  const int ns = (e + a.split_len - 1) / a.split_len;
+  if (ns <= 1) return;
+  const int b = bh / a.heads, h = bh - b * a.heads;
+  uint16_t* op = a.o + b * a.so.b + h * a.so.h;
+  const int64_t slot0 = ((int64_t)bh * a.q_tiles + qt) * a.n_splits;
+  const int tid = wi_x();
+  const int d0 = 4 * (tid & 15);
+  constexpr int kG = 8;
+#pragma unroll
+  for (int pass = 0; pass < 2; ++pass) {
+    const int row = pass * 16 + (tid >> 4);
+    if (i0 + row >= a.q_len) continue;
+    const float* lp = a.part_lse + slot0 * 32 + row;                  // split s: lp[32 s]
+    const float* pp = a.part_o + (slot0 * 32 + row) * kHeadDim + d0;  // split s: pp[32 * 64 s]
+    float mm = -INFINITY, wt = 0.f;
+    f32x4 acc = {};
+    for (int s0 = 0; s0 < ns; s0 += kG) {
+      float l[kG];
+#pragma unroll
+      for (int k = 0; k < kG; ++k) l[k] = s0 + k < ns ? lp[(s0 + k) * 32] : -INFINITY;
+#pragma unroll
+      for (int k = 0; k < kG; ++k) mm = fmaxf(mm, l[k]);
+    }
+    for (int s0 = 0; s0 < ns; s0 += kG) {
+      float l[kG];
+      f32x4 po[kG];
+#pragma unroll
+      for (int k = 0; k < kG; ++k) {
+        if (s0 + k < ns) {
+          l[k] = lp[(s0 + k) * 32];
+          po[k] = *reinterpret_cast<const f32x4*>(pp + (s0 + k) * 32 * kHeadDim);
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < kG; ++k) {
+        if (s0 + k < ns) {
+          const float w = fast_exp2(l[k] - mm);  // a split the row does not see: 0
+          wt += w;
+          acc += w * po[k];
+        }
+      }
+    }
+    const float inv = 1.f / wt;
+    *reinterpret_cast<bf16x4*>(op + (int64_t)(i0 + row) * a.so.s + d0) =
+        to_bf16x4(acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv);
+  }
 }
 
 }  // namespace
@@ -279,6 +452,24 @@ hipError_t launch_attn_fwd(const FwdArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL((attn_fwd_dma_kernel<BD3_FWD_OCC, true>), grid, block, 0, stream, a);
   else
     hipLaunchKernelGGL((attn_fwd_dma_kernel<BD3_FWD_OCC, false>), grid, block, 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_prefill(const DecodeArgs& a, hipStream_t stream) {
+  // Items (batch*head, split, 128-row tile), longest rows first; splits past
+  // the last key and those a tile does not reach exit at once.
+  const int row_tiles = (a.q_len + 127) / 128;
+  const int splits = (a.kv_len + a.split_len - 1) / a.split_len;
+  const dim3 grid(a.bh, splits, row_tiles), block(256);
+  if (a.bs % 16 == 0 && a.kv_len % 16 == 0)
+    hipLaunchKernelGGL((prefill_attn_kernel<BD3_FWD_OCC, true>), grid, block, 0, stream, a);
+  else
+    hipLaunchKernelGGL((prefill_attn_kernel<BD3_FWD_OCC, false>), grid, block, 0, stream, a);
+  hipError_t e = hipGetLastError();
+  // The last tile sees the most keys: if they fit one split, no partials.
+  if (e != hipSuccess || decode_key_end(128 * (row_tiles - 1), 128, a.q_len, a.kv_len, a.bs) <= a.split_len)
+    return e;
+  hipLaunchKernelGGL(prefill_combine, dim3(a.q_tiles, a.bh), block, 0, stream, a);
   return hipGetLastError();
 }
 

@@ -109,6 +109,16 @@ __device__ __forceinline__ float shfl_xor(float x, int m) {
   return __shfl_xor(x, m, 64);
 }
 
+// Work-item and workgroup ids read from the hardware-initialised registers.
+// threadIdx / blockIdx go through calls to the device library's
+// __ockl_get_local_id / __ockl_get_group_id, which this toolchain leaves out
+// of line at -O3 (an s_swappc and the call ABI's register conventions in
+// every kernel prologue).
+__device__ __forceinline__ int wi_x() { return (int)__builtin_amdgcn_workitem_id_x(); }
+__device__ __forceinline__ int wg_x() { return (int)__builtin_amdgcn_workgroup_id_x(); }
+__device__ __forceinline__ int wg_y() { return (int)__builtin_amdgcn_workgroup_id_y(); }
+__device__ __forceinline__ int wg_z() { return (int)__builtin_amdgcn_workgroup_id_z(); }
+
 // A value the program knows to be the same in every lane of the wave (the
 // wave index, tile counts derived from blockIdx): moving it to an SGPR lets
 // the compiler branch on it with scalar branches instead of exec masks.

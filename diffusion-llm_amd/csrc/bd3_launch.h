@@ -134,6 +134,7 @@ hipError_t launch_attn_fwd(const FwdArgs& a, hipStream_t stream);
 hipError_t launch_attn_bwd_dq(const BwdArgs& a, hipStream_t stream);
 hipError_t launch_attn_bwd_dkdv(const BwdArgs& a, hipStream_t stream);
 hipError_t launch_decode(const DecodeArgs& a, int qt, hipStream_t stream);
+hipError_t launch_prefill(const DecodeArgs& a, hipStream_t stream);
 hipError_t launch_qkv_rope(const QkvRopeArgs& a, hipStream_t stream);
 hipError_t launch_kv_write(const KvWriteArgs& a, hipStream_t stream);
 hipError_t launch_subs_sample(const SubsArgs& a, hipStream_t stream);

@@ -53,15 +53,16 @@ __device__ __forceinline__ bool iv_has(const RowIntervals& iv, int k) {
          ((unsigned)(k - iv.lo2) < (unsigned)(iv.hi2 - iv.lo2));
 }
 
-// Work order shared by the training kernels: blockIdx.x -> (rank, bh) with
+// Work order shared by the training kernels: workgroup id -> (rank, bh) with
 // bh fastest, so that every tile of one (b, h) lands on the same XCD when
 // bh % 8 == 0 (workgroups are dealt to the 8 XCDs round-robin); rank 0 is the
 // heaviest tile.
 struct BlockOrder {
   int rank, bh, b, h;
-  __device__ __forceinline__ BlockOrder(int bhs, int heads) {
-    rank = blockIdx.x / bhs;
-    bh = blockIdx.x - rank * bhs;
+  __device__ __forceinline__ BlockOrder(int bhs, int heads) : BlockOrder(wg_x(), bhs, heads) {}
+  __device__ __forceinline__ BlockOrder(int id, int bhs, int heads) {
+    rank = id / bhs;
+    bh = id - rank * bhs;
     b = bh / heads;
     h = bh - b * heads;
   }

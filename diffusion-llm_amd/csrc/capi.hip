@@ -120,7 +120,37 @@ bd3::BwdArgs bwd_args(const void* q, const void* k, const void* v, const void* o
   return a;
 }
 
+// Above this many queries the decode call runs the prefill kernel (128-row
+// query tiles sharing each K / V tile; the decode kernels re-read the keys
+// once per 32 rows).
+constexpr int kPrefillMinQ = 65;
+
+// Splits for the prefill kernel: as few as keep the longest item (one split
+// of one 128-row tile) under the grid's total work spread over the GPU at
+// full occupancy (3 workgroups per CU on 256 CUs), with kLoneTile = the cost
+// of a 64-key tile in a workgroup running alone on its CU relative to one of
+// three sharing the CU. Work is counted in 64-key tiles at block size 1 (the
+// most keys any block size allows).
+int32_t prefill_auto_splits(int32_t batch, int32_t heads, int32_t q_len, int32_t kv_len) {
+  constexpr double kSlots = 768.0, kLoneTile = 0.43;
+  const int row_tiles = (q_len + 127) / 128;
+  int64_t tiles = 0;
+  for (int t = 0; t < row_tiles; ++t) {
+    const int64_t e = (int64_t)kv_len - q_len + (128 * (t + 1) < q_len ? 128 * (t + 1) : q_len);
+    tiles += (e + 63) / 64;
+  }
+  tiles *= (int64_t)batch * heads;
+  double longest = (double)tiles / kSlots / kLoneTile;  // tiles one item may take
+  if (longest < 4.0) longest = 4.0;
+  const int64_t kv_tiles = ((int64_t)kv_len + 63) / 64;
+  int64_t s = (int64_t)((double)kv_tiles / longest + 0.999999);
+  if (s < 1) s = 1;
+  if (s > 64) s = 64;
+  return (int32_t)s;
+}
+
 int32_t auto_splits(int32_t batch, int32_t heads, int32_t q_len, int32_t kv_len) {
+  if (q_len >= kPrefillMinQ) return prefill_auto_splits(batch, heads, q_len, kv_len);
   // At least one workgroup per CU on a 256-CU part; beyond that more splits
   // only add partial traffic and a merge launch. Never fewer than 512 keys
   // per split for q_len > 16 (32-row tiles): below that the merge launch
@@ -199,6 +229,19 @@ int run_decode(const void* q, const void* k, const void* v, void* o, int32_t bat
     }
   }
   a.scale_log2 = scale * bd3::kLog2e;
+  if (q_len >= kPrefillMinQ) {
+    // 128-row tiles, splits of whole 64-key tiles; partials in the same
+    // layout (one slot per 32-row tile and split).
+    for (int i = 1; i <= 2; ++i) {
+      const int st = check_dma_stride(strides + 3 * i, i == 1 ? "k" : "v");
+      if (st) return st;
+    }
+    int pl = (kv_len + n_splits - 1) / n_splits;
+    a.split_len = (pl + 63) / 64 * 64;
+    a.groups = n_splits;
+    a.splits_per_group = 1;
+    return hip_status(bd3::launch_prefill(a, static_cast<hipStream_t>(stream)), "prefill launch");
+  }
   return hip_status(bd3::launch_decode(a, kDecodeQT, static_cast<hipStream_t>(stream)), "decode launch");
 }
 

@@ -158,8 +158,12 @@ int bd3_attn_bwd_dkdv(const void* q, const void* k, const void* v,
  * n_splits = 0 lets the library choose a key split that fills the GPU
  * (a workspace of bd3_decode_workspace_bytes(..., 0, ...) is then needed;
  * pass NULL/0 when that size is 0).
+ * q_len > 64 (a long query block or a whole-sequence prefill) runs a
+ * kernel with 128-row query tiles sharing each K / V tile.
  * strides: 12 int64 = (b, h, s) element strides of q, k, v, o.
- * Preconditions: 1 <= q_len <= kv_len, head_dim == 64, block_size >= 1.
+ * Preconditions: 1 <= q_len <= kv_len, head_dim == 64, block_size >= 1;
+ * for q_len > 64 the k and v sequence strides are below 2^24 elements
+ * (32-bit per-lane tile load offsets).
  *
  * Replaces block_sparse_decode_kern and its launch in
  * block_sparse_decode_attention
@@ -198,7 +202,8 @@ size_t bd3_decode_workspace_bytes(int32_t batch, int32_t heads, int32_t q_len,
  * (kernels/SplitKVDecodeAttention.py:147); callers pass it explicitly.
  * strides: 12 int64 = (b, h, s) element strides of q, k, v, o.
  * Preconditions: 1 <= q_len <= kv_len, head_dim == 64,
- * 1 <= n_splits <= kv_len, workspace large enough.
+ * 1 <= n_splits <= kv_len, workspace large enough; for q_len > 64 the k
+ * and v sequence strides are below 2^24 elements (as bd3_decode).
  *
  * Replaces split_kv_kern + split_kv_reduce_kern and their launches in
  * split_kv_decode_attention (kernels/SplitKVDecodeAttention.py:16-171).

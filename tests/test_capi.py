@@ -197,6 +197,12 @@ def test_tile_load_offset_stride_limit(lib):
         st18[3 * slot + 2] = big
         expect_einval(lib.bd3_attn_bwd_dkdv(*[GOOD] * 8, 1, 1, 128, 64, 16, _i64(st18), 0.125, None),
                       f"{name} sequence stride")
+    # decode with q_len > 64 runs the prefill kernel, which loads k and v tile by tile
+    for slot, name in ((1, "k"), (2, "v")):
+        st = [64 * 4096, 64 * 4096, 64] * 4
+        st[3 * slot + 2] = big
+        expect_einval(lib.bd3_decode_splitkv(GOOD, GOOD, GOOD, GOOD, 1, 1, 65, 4096, 64, 16, 1, _i64(st), 0.125,
+                                             None, 0, None), f"{name} sequence stride")
     # q's stride in the forward is not a tile-load offset: only the 8-alignment applies
     st = [big - 8, 64, 64] + ok * 3
     status = lib.bd3_attn_fwd(GOOD, GOOD, GOOD, GOOD, None, 1, 1, 128, 64, 16, _i64(st), 0.125, None)
@@ -230,6 +236,13 @@ def test_workspace_sizes(lib):
     # a cached step (q_len <= 16): down to 128 keys per split, at most 16 splits
     assert [lib.bd3_decode_auto_splits(1, 12, 16, kv) for kv in (200, 544, 3584, 8192)] == [1, 4, 16, 16]
     assert lib.bd3_decode_auto_splits(2, 12, 16, 1024) == 8
+    # q_len > 64 (the prefill kernel): split only until the longest item is
+    # no longer than the whole grid's share per slot allows
+    assert lib.bd3_decode_auto_splits(1, 12, 3088, 3088) == 3
+    assert lib.bd3_decode_auto_splits(8, 12, 2048, 2048) == 1
+    assert lib.bd3_decode_auto_splits(32, 12, 128, 4112) == 1
+    assert lib.bd3_decode_auto_splits(4, 12, 256, 4096) == 4
+    assert lib.bd3_decode_auto_splits(1, 12, 128, 3584) == 14
     assert lib.bd3_decode_workspace_bytes(32, 12, 16, 4112, 64, 0) == lib.bd3_decode_workspace_bytes(
         32, 12, 16, 4112, 64, s)
 

@@ -93,6 +93,36 @@ def test_config3_split_invariance(cuda):
         assert max_abs(o, outs[0]) <= 1e-2
 
 
+# q_len > 64 runs the prefill kernel: 128-row query tiles, splits of whole
+# 64-key tiles, row tiles whose keys fit the first split written directly and
+# the others merged from partials; empty trailing splits; ragged last key
+# and row tiles; per-element masks (bs or kv_len not multiples of 16).
+PREFILL = [(1, 2, 1000, 1000, 16), (2, 3, 333, 2000, 5), (1, 2, 129, 4000, 32), (1, 1, 65, 65, 1),
+           (1, 12, 3088, 3088, 16), (2, 2, 512, 1030, 16)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,H,q_len,kv_len,bs", PREFILL)
+def test_prefill_splits_match_oracle(cuda, record_error, B, H, q_len, kv_len, bs):
+    q, k, v = decode_inputs(B, H, q_len, kv_len, seed=3 * q_len + kv_len)
+    ref = decode_attention(q, k, v, bs)
+    dq, dk, dv = (t.to(cuda, torch.bfloat16) for t in (q, k, v))
+    outs = {}
+    for ns in (1, 2, 3, 7, 40):
+        if ns > kv_len:
+            continue
+        print(f"prefill B={B} H={H} q_len={q_len} kv_len={kv_len} bs={bs} splits={ns}", flush=True)
+        outs[ns] = splitkv_capi(dq, dk, dv, bs, ns)
+    auto = block_sparse_decode_attention(dq, dk, dv, bs)
+    torch.cuda.synchronize()
+    for ns, o in outs.items():
+        record_error(f"prefill O max-abs ({ns} splits)", max_abs(o, ref), OUT_TOL)
+        # a split changes each P's bf16 rounding (its running maximum
+        # differs) and the fp32 merge, nothing else
+        assert max_abs(o, outs[1]) <= 1e-2, f"{ns} splits vs one"
+    record_error("prefill O max-abs (auto splits)", max_abs(auto, ref), OUT_TOL)
+
+
 @pytest.mark.gpu
 def test_decode_strided_cache_view(cuda):
     """K/V read in place from a larger preallocated cache (outer strides of a

@@ -159,8 +159,15 @@ DECODE = [  # (q_len, kv_len, block size, split counts)
     (32, 2048, 32, (1, 3, 4)),
     (40, 1337, 4, (1, 2, 5)),
     (64, 777, 64, (1, 3)),
-    (256, 2048, 256, (1,)),
-    (300, 300, 16, (1,)),  # prefill: q_len == kv_len
+    # q_len > 64: the prefill kernel (128-row tiles, splits of whole 64-key
+    # tiles; single-split row tiles write O, the others go through partials)
+    (256, 2048, 256, (1, 3)),
+    (300, 300, 16, (1, 2, 5)),  # q_len == kv_len
+    (1000, 1000, 16, (1, 3)),  # row tiles 0-2 in the first split, 3-7 merged
+    (100, 777, 7, (1, 2, 4)),  # per-element mask, ragged last key tile
+    (65, 2048, 32, (1, 5)),  # the tile's last three waves hold one row, then none
+    (129, 129, 1, (1, 2)),  # a second row tile holding one row
+    (200, 1000, 48, (1, 3, 16)),  # kv_len % 16 != 0: per-element mask; empty splits
 ]
 
 
