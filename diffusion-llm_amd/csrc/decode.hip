@@ -58,18 +58,18 @@ constexpr size_t kSmemBytes = kVBytes > sizeof(MergeLds) ? kVBytes : sizeof(Merg
 
 __global__ __launch_bounds__(kThreads) void decode_partial(DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[kSmemBytes];
-  __bf16* ks = reinterpret_cast<__bf16*>(smem) + (threadIdx.x >> 6) * 2 * kSub * kStride;
+  __bf16* ks = reinterpret_cast<__bf16*>(smem) + (wi_x() >> 6) * 2 * kSub * kStride;
   __bf16* vs = ks + kSub * kStride;
 
-  const int tid = threadIdx.x;
+  const int tid = wi_x();
   const int lane = tid & 63;
   const int wave = wave_uniform(tid >> 6);
   const int l32 = lane & 31;
   const int g = lane >> 5;
 
-  const int split = blockIdx.x;
-  const int qt = blockIdx.y;
-  const int bh = blockIdx.z;
+  const int split = wg_x();
+  const int qt = wg_y();
+  const int bh = wg_z();
   const int b = bh / a.heads, h = bh - b * a.heads;
   const int i0 = qt * kQT;
 
@@ -268,7 +268,7 @@ template <int NW>
 __global__ __launch_bounds__(NW * 64, BD3_DEC16_OCC) void decode16_partial(DecodeArgs a) {
   constexpr int kNT = NW * 64;
   __shared__ __attribute__((aligned(16))) char smem[smem16_bytes<NW>()];
-  const int tid = threadIdx.x;
+  const int tid = wi_x();
   const int lane = tid & 63;
   const int wave = wave_uniform(tid >> 6);
   const int l16 = lane & 15;
@@ -276,8 +276,8 @@ __global__ __launch_bounds__(NW * 64, BD3_DEC16_OCC) void decode16_partial(Decod
   __bf16* ks = reinterpret_cast<__bf16*>(smem) + wave * 2 * kTile16;
   __bf16* vs = ks + kTile16;
 
-  const int grp = blockIdx.x;
-  const int bh = blockIdx.z;
+  const int grp = wg_x();
+  const int bh = wg_z();
   const int b = bh / a.heads, h = bh - b * a.heads;
   const uint16_t* qp = a.q + b * a.sq.b + h * a.sq.h;
   const uint16_t* kp = a.k + b * a.sk.b + h * a.sk.h;
@@ -541,16 +541,16 @@ __global__ __launch_bounds__(NW * 64, BD3_DEC16_OCC) void decode16_partial(Decod
 // before the first use (one memory round trip); NS == 0 takes any count.
 template <int NS>
 __global__ __launch_bounds__(kThreads) void decode_combine(DecodeArgs a) {
-  const int qt = blockIdx.x;
-  const int bh = blockIdx.y;
+  const int qt = wg_x();
+  const int bh = wg_y();
   const int b = bh / a.heads, h = bh - b * a.heads;
   const int i0 = qt * kQT;
   uint16_t* op = a.o + b * a.so.b + h * a.so.h;
   const int64_t slot0 = ((int64_t)bh * a.q_tiles + qt) * a.groups;
-  const int d0 = 4 * (threadIdx.x & 15);
+  const int d0 = 4 * (wi_x() & 15);
 #pragma unroll
   for (int pass = 0; pass < kQT / 16; ++pass) {
-    const int row = pass * 16 + (threadIdx.x >> 4);
+    const int row = pass * 16 + (wi_x() >> 4);
     if (i0 + row >= a.q_len) continue;
     const float* lp = a.part_lse + slot0 * kQT + row;                  // split s: lp[s * kQT]
     const float* pp = a.part_o + (slot0 * kQT + row) * kHeadDim + d0;  // split s: pp[s * kQT * kHeadDim]
@@ -619,7 +619,7 @@ __global__ __launch_bounds__(kThreads) void decode_combine(DecodeArgs a) {
 
 __global__ void mask_dump_kernel(uint8_t* out, int mode, int rows, int cols, int kv_len,
                                  int bs) {
-  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t e = (int64_t)wg_x() * 256 + wi_x();
   if (e >= (int64_t)rows * cols) return;
   const int i = (int)(e / cols), j = (int)(e - (int64_t)i * cols);
   bool vis;

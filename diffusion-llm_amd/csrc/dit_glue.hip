@@ -121,9 +121,9 @@ __device__ __forceinline__ void ln_modulate_row(const GlueArgs& a, int b, int s,
 // from HBM once into registers (d_model <= 512 * CH).
 template <int CH>
 __global__ __launch_bounds__(256) void ln_modulate_kernel(GlueArgs a) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int row = wg_x() * 4 + (wi_x() >> 6);
   if (row >= a.rows) return;
-  const int lane = threadIdx.x & 63;
+  const int lane = wi_x() & 63;
   const int b = row / a.seq, s = row - b * a.seq;
   const int nch = a.d >> 3;
   const void* xr = elem(a.x, a.x_fp32, b * a.sx_b + s * a.sx_s);
@@ -149,9 +149,9 @@ __global__ __launch_bounds__(256) void ln_modulate_kernel(GlueArgs a) {
 template <int CH>
 __global__ __launch_bounds__(256) void gate_residual_ln_modulate_kernel(GlueArgs a) {
 #pragma clang fp contract(off)  // gate * y rounded before the add, as the eager ops
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int row = wg_x() * 4 + (wi_x() >> 6);
   if (row >= a.rows) return;
-  const int lane = threadIdx.x & 63;
+  const int lane = wi_x() & 63;
   const int b = row / a.seq, s = row - b * a.seq;
   const int nch = a.d >> 3;
   const bool gy_bf16 = !a.m_fp32 && !a.y_fp32;
@@ -187,7 +187,7 @@ __global__ __launch_bounds__(256) void gate_residual_ln_modulate_kernel(GlueArgs
 
 __global__ __launch_bounds__(256) void gate_residual_kernel(GlueArgs a) {
 #pragma clang fp contract(off)  // gate * y rounded before the add, as the eager ops
-  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;  // one 8-element chunk
+  const int64_t e = (int64_t)wg_x() * 256 + wi_x();  // one 8-element chunk
   const int nch = a.d >> 3;
   if (e >= (int64_t)a.rows * nch) return;
   const int row = (int)(e / nch), c = (int)(e - (int64_t)row * nch);

@@ -71,7 +71,7 @@ __device__ __forceinline__ void rotate8(const u32x4& x1, const u32x4& x2, const 
 // 8-pair slice of the sin / cos rows, shared by q and k. Four consecutive
 // items cover a head's rows.
 __global__ __launch_bounds__(256) void qkv_rope_kernel(QkvRopeArgs a) {
-  const uint32_t e = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t e = wg_x() * 256u + wi_x();
   if (e >= (uint32_t)a.total) return;
   const uint32_t per_tok = 4u * (uint32_t)a.heads;
   const uint32_t tok = e / per_tok;
@@ -114,7 +114,7 @@ __global__ __launch_bounds__(256) void qkv_rope_kernel(QkvRopeArgs a) {
 
 // One thread per 16 bytes of a head row: 8 threads per (tensor, b, h, s).
 __global__ __launch_bounds__(256) void kv_write_kernel(KvWriteArgs a) {
-  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t e = (int64_t)wg_x() * 256 + wi_x();
   if (e >= a.total) return;
   const int part = (int)(e & 7);
   int64_t row = e >> 3;  // over (tensor, b, h, s)
