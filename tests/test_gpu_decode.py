@@ -124,12 +124,19 @@ def test_prefill_splits_match_oracle(cuda, record_error, B, H, q_len, kv_len, bs
 
 
 @pytest.mark.gpu
-def test_decode_strided_cache_view(cuda):
-    """K/V read in place from a larger preallocated cache (outer strides of a
-    (B, H, L_max, d) buffer) equal the contiguous result."""
-    B, H, q_len, kv_len, L_max, bs = 2, 3, 16, 500, 1024, 16
-    kc = torch.randn(B, H, L_max, 64, device=cuda, dtype=torch.bfloat16)
-    vc = torch.randn(B, H, L_max, 64, device=cuda, dtype=torch.bfloat16)
+@pytest.mark.parametrize("layout", ["bhsd", "bshd"])
+@pytest.mark.parametrize("q_len", [16, 300])
+def test_decode_strided_cache_view(cuda, q_len, layout):
+    """K/V read in place from a larger preallocated cache equal the
+    contiguous result, for the decode kernel (q_len 16) and the prefill
+    kernel (q_len 300, tile loads): a (B, H, L_max, d) buffer (outer strides)
+    or a (B, L_max, H, d) one (sequence stride H * d)."""
+    B, H, kv_len, L_max, bs = 2, 3, 500, 1024, 16
+    shape = (B, H, L_max, 64) if layout == "bhsd" else (B, L_max, H, 64)
+    kc = torch.randn(shape, device=cuda, dtype=torch.bfloat16)
+    vc = torch.randn(shape, device=cuda, dtype=torch.bfloat16)
+    if layout == "bshd":
+        kc, vc = kc.transpose(1, 2), vc.transpose(1, 2)
     q = torch.randn(B, H, q_len, 64, device=cuda, dtype=torch.bfloat16)
     o1 = block_sparse_decode_attention(q, kc[:, :, :kv_len], vc[:, :, :kv_len], bs)
     o2 = block_sparse_decode_attention(q, kc[:, :, :kv_len].contiguous(),
