@@ -26,7 +26,11 @@ def rnd(shape, dtype, seed, scale=1.0, shift=0.0):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("xd,md,od", [(F32, BF, F32), (F32, BF, BF), (BF, BF, BF), (BF, F32, F32), (F32, F32, F32)])
-@pytest.mark.parametrize("B,S,D", [(2, 37, 768), (1, 5, 64), (8, 256, 768)])
+# Rows per wave: 4 up to d = 1024, 2 up to 2048, 1 beyond; sequence lengths
+# that are not multiples of that put two batch indices in one wave; d = 520
+# leaves one lane with a second, last chunk.
+@pytest.mark.parametrize("B,S,D", [(2, 37, 768), (1, 5, 64), (8, 256, 768), (2, 9, 2048), (3, 7, 4096),
+                                   (2, 11, 520)])
 def test_ln_modulate(cuda, xd, md, od, B, S, D):
     print(f"ln_modulate x={xd} mod={md} out={od} shape=({B},{S},{D})", flush=True)
     x = rnd((B, S, D), xd, 1, scale=2.0, shift=0.3)
@@ -52,8 +56,8 @@ def test_ln_modulate(cuda, xd, md, od, B, S, D):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("xd,gd,yd", [(F32, BF, BF), (BF, BF, BF), (F32, F32, F32), (BF, F32, BF)])
-def test_gate_residual_bit_exact(cuda, xd, gd, yd):
-    B, S, D = 3, 50, 768
+@pytest.mark.parametrize("B,S,D", [(3, 50, 768), (2, 7, 520), (1, 3, 64)])
+def test_gate_residual_bit_exact(cuda, xd, gd, yd, B, S, D):
     x, g, y = rnd((B, S, D), xd, 5), rnd((B, D), gd, 6), rnd((B, S, D), yd, 7)
     want = ref_gate(x, g, y)
     got = gate_residual(x.to(cuda), g.to(cuda)[:, None], y.to(cuda)).cpu()
@@ -72,7 +76,7 @@ def test_gate_residual_in_place(cuda):
 @pytest.mark.gpu
 @pytest.mark.parametrize("xd,md,yd,od", [(BF, BF, BF, BF), (F32, BF, BF, None), (F32, BF, BF, BF),
                                          (BF, F32, BF, None), (F32, F32, F32, None)])
-@pytest.mark.parametrize("B,S,D", [(2, 37, 768), (1, 5, 64), (3, 2, 4096)])
+@pytest.mark.parametrize("B,S,D", [(2, 37, 768), (1, 5, 64), (3, 2, 4096), (2, 9, 2048), (2, 11, 520)])
 def test_gate_residual_ln_modulate_matches_two_calls(cuda, xd, md, yd, od, B, S, D):
     """The fused residual + LayerNorm + modulate equals gate_residual followed
     by ln_modulate bit for bit (same kernels' arithmetic, one launch), both
