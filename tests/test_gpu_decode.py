@@ -123,6 +123,32 @@ def test_prefill_splits_match_oracle(cuda, record_error, B, H, q_len, kv_len, bs
     record_error("prefill O max-abs (auto splits)", max_abs(auto, ref), OUT_TOL)
 
 
+def _random_prefill_shapes(count: int, seed: int):
+    """(B, H, q_len, kv_len, bs, n_splits) drawn from a fixed generator:
+    q_len 65-700 (the prefill kernel), a cached prefix of 0-1500 keys, block
+    sizes 1-300, split counts 1-24 (many of them past the last key tile)."""
+    import random
+    r = random.Random(seed)
+    out = []
+    for _ in range(count):
+        q_len = r.randint(65, 700)
+        kv_len = q_len + r.choice([0, 0, r.randint(1, 1500)])
+        out.append((r.randint(1, 2), r.randint(1, 3), q_len, kv_len, r.choice([1, 3, 7, 16, 32, 48, 64, 100, 300]),
+                    r.randint(1, 24)))
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,H,q_len,kv_len,bs,n_splits", _random_prefill_shapes(16, seed=2026))
+def test_prefill_random_shapes(cuda, record_error, B, H, q_len, kv_len, bs, n_splits):
+    print(f"prefill random B={B} H={H} q_len={q_len} kv_len={kv_len} bs={bs} splits={n_splits}", flush=True)
+    q, k, v = decode_inputs(B, H, q_len, kv_len, seed=q_len * 7 + kv_len)
+    o = splitkv_capi(*(t.to(cuda, torch.bfloat16) for t in (q, k, v)), bs, n_splits)
+    ref = decode_attention(q, k, v, bs)
+    torch.cuda.synchronize()
+    record_error("prefill O max-abs (random shapes)", max_abs(o, ref), OUT_TOL)
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("layout", ["bhsd", "bshd"])
 @pytest.mark.parametrize("q_len", [16, 300])
