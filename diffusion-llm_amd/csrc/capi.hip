@@ -151,25 +151,27 @@ int32_t prefill_auto_splits(int32_t batch, int32_t heads, int32_t q_len, int32_t
 
 int32_t auto_splits(int32_t batch, int32_t heads, int32_t q_len, int32_t kv_len) {
   if (q_len >= kPrefillMinQ) return prefill_auto_splits(batch, heads, q_len, kv_len);
-  // At least one workgroup per CU on a 256-CU part; beyond that more splits
-  // only add partial traffic and a merge launch. Never fewer than 512 keys
-  // per split for q_len > 16 (32-row tiles): below that the merge launch
-  // costs more than the extra workgroups gain. Measured at configs[3] (384
-  // workgroups at one split): 66 us at one split, 68 us at two (including the
-  // merge), 71 us at three; at 8 x 12 heads, q_len 32: kv_len 544 12.4 us at
-  // one split vs 14.6 at three, kv_len 1056 16.4 / 16.1 / 16.7 us at one /
-  // two / three, kv_len 2080 24.3 / 20.5 / 21.3 / 20.6 us at one to four.
-  // A cached step (q_len <= 16) merges its splits in one memory round trip
-  // and pays for splits down to 128 keys, up to 16 of them: 16 queries over a
-  // 3584-token cache, batch 1, 12 heads: 12.7 us at 7 splits, 11.8 at 14 or
-  // 16, 12.5-12.9 at 21-28; over 8192 tokens 16.2 / 13.9 / 15.3 / 15.2 us at
-  // 8 / 16 / 22 / 32; batch 2, 12 heads, over 1024 tokens 11.6 / 11.1 / 10.5
-  // / 11.0 us at 2 / 4 / 8 / 11.
+  // A cached step (q_len <= 16, 16-row tiles): at least one workgroup per CU
+  // on a 256-CU part; beyond that more splits only add partial traffic and a
+  // merge launch. Measured at configs[3] (384 workgroups at one split): 66 us
+  // at one split, 68 us at two (including the merge), 71 us at three. Its
+  // merge of up to 32 splits is one memory round trip, so it pays for splits
+  // down to 128 keys, up to 16 of them: 16 queries over a 3584-token cache,
+  // batch 1, 12 heads: 12.7 us at 7 splits, 11.8 at 14 or 16, 12.5-12.9 at
+  // 21-28; over 8192 tokens 16.2 / 13.9 / 15.3 / 15.2 us at 8 / 16 / 22 /
+  // 32; batch 2, 12 heads, over 1024 tokens 11.6 / 11.1 / 10.5 / 11.0 us at
+  // 2 / 4 / 8 / 11.
+  // 32-row tiles (16 < q_len <= 64), whose workgroups take 8 waves when there
+  // are fewer than 256 of them: about 128 workgroups, and at least 1024 keys
+  // per split once there are 64 or more tiles (512 with fewer; the merge
+  // launch costs more than a shorter chain saves): at 8 x 12 heads, q_len 32,
+  // 2048 keys 16.8 us at 2 splits vs 17.8 at 1 and 19.3 at 3; 1024 keys 12.0
+  // at 1 vs 13.7 at 2; batch 1 over 3584 keys 13.3-13.6 at 7-8 splits.
   const int64_t base = (int64_t)batch * heads * decode_q_tiles(q_len);
-  const int64_t target = 256;
+  const int64_t target = q_len <= 16 ? 256 : 128;
   int64_t s = (target + base - 1) / base;
   if (q_len <= 16 && s > 16) s = 16;
-  const int min_keys = q_len <= 16 ? 128 : 512;
+  const int min_keys = q_len <= 16 ? 128 : (base >= 64 ? 1024 : 512);
   const int64_t max_by_len = kv_len / min_keys > 0 ? kv_len / min_keys : 1;
   if (s > max_by_len) s = max_by_len;
   if (s < 1) s = 1;

@@ -6,9 +6,10 @@
 // j / bs <= (kv_len - q_len + i) / bs and j < kv_len (bd3_mask.h).
 //
 // decode_partial: one workgroup per (split, 32-row query tile, batch*head).
-//   The split's key range is cut into 32-key chunks that the four waves take
-//   in turn; each wave runs an online softmax over its chunks, then the four
-//   states are merged through LDS. With one split the workgroup writes O
+//   The split's key range is cut into 32-key chunks that the waves (four, or
+//   eight when the grid has fewer workgroups than CUs and a split holds at
+//   least 16 chunks) take in turn; each wave runs an online softmax over its
+//   chunks, then the waves' states are merged through LDS. With one split the workgroup writes O
 //   directly; otherwise it writes a normalised fp32 partial and its log2-LSE.
 //   K and V are read once per call, with non-temporal loads (ld16_stream) so
 //   the stream does not evict other data from L2 / MALL; measured 7% faster
@@ -43,21 +44,30 @@ namespace {
 
 constexpr int kNW = 4;
 constexpr int kThreads = kNW * 64;
+
 constexpr int kQT = 32;       // query rows per workgroup
 constexpr int kSub = 32;      // keys per wave step
 constexpr int kStride = 72;   // padded LDS row (bf16)
 constexpr int kVElems = 2 * kSub * kStride;  // a wave's K and V tiles
 
+template <int NW>
 struct MergeLds {
-  float o[kNW][kHeadDim][kQT + 1];  // O^T per wave (unnormalised), padded
-  float m[kNW][kQT];
-  float l[kNW][kQT];
+  float o[NW][kHeadDim][kQT + 1];  // O^T per wave (unnormalised), padded
+  float m[NW][kQT];
+  float l[NW][kQT];
 };
-constexpr size_t kVBytes = sizeof(__bf16) * kNW * kVElems;
-constexpr size_t kSmemBytes = kVBytes > sizeof(MergeLds) ? kVBytes : sizeof(MergeLds);
+template <int NW>
+constexpr size_t partial_smem_bytes() {
+  constexpr size_t v = sizeof(__bf16) * NW * kVElems;
+  return v > sizeof(MergeLds<NW>) ? v : sizeof(MergeLds<NW>);
+}
 
-__global__ __launch_bounds__(kThreads) void decode_partial(DecodeArgs a) {
-  __shared__ __attribute__((aligned(16))) char smem[kSmemBytes];
+// NW waves share the key chunks of one (split, 32-row tile, batch*head).
+template <int NW>
+__global__ __launch_bounds__(NW * 64) void decode_partial(DecodeArgs a) {
+  constexpr int kNW = NW;
+  constexpr int kThreads = NW * 64;
+  __shared__ __attribute__((aligned(16))) char smem[partial_smem_bytes<NW>()];
   __bf16* ks = reinterpret_cast<__bf16*>(smem) + (wi_x() >> 6) * 2 * kSub * kStride;
   __bf16* vs = ks + kSub * kStride;
 
@@ -182,7 +192,7 @@ __global__ __launch_bounds__(kThreads) void decode_partial(DecodeArgs a) {
   // Merge the four waves' states.
   lsum = sum_xor32(lsum);
   __syncthreads();  // V staging area is reused below
-  MergeLds* ml = reinterpret_cast<MergeLds*>(smem);
+  MergeLds<NW>* ml = reinterpret_cast<MergeLds<NW>*>(smem);
 #pragma unroll
   for (int db = 0; db < 2; ++db)
 #pragma unroll
@@ -637,8 +647,14 @@ hipError_t launch_decode(const DecodeArgs& a, int /*qt*/, hipStream_t stream) {
   dim3 grid(a.groups, a.q_tiles, a.bh);
   if (a.q_len <= kQ16)
     hipLaunchKernelGGL(decode16_partial<kNW>, grid, dim3(kThreads), 0, stream, a);
+  else if ((int64_t)a.bh * a.q_tiles * a.groups < 256 && a.split_len >= 512)
+    // Fewer workgroups than CUs, each with at least 16 chunks: 8 waves share
+    // them (measured at 8 x 12 heads, q_len 32, one split: 2048 keys 20.9 ->
+    // 17.8 us, 1024 keys 13.4 -> 12.0; batch 1 over 3584 keys 30.1 -> 22.3;
+    // with 128 keys per split 4 waves stay faster, 7.1 vs 7.6 us).
+    hipLaunchKernelGGL(decode_partial<8>, grid, dim3(8 * 64), 0, stream, a);
   else
-    hipLaunchKernelGGL(decode_partial, grid, dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL(decode_partial<kNW>, grid, dim3(kThreads), 0, stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.groups == 1) return e;
   const dim3 cgrid(a.q_tiles, a.bh);

@@ -231,8 +231,10 @@ def test_workspace_sizes(lib):
     assert lib.bd3_decode_workspace_bytes(2, 3, 16, 100, 64, 4) == slots * 64 * 4 + ((slots * 4 + 255) // 256) * 256
     s = lib.bd3_decode_auto_splits(32, 12, 16, 4112)
     assert s == 1  # 384 workgroups at one split already cover 256 CUs
-    # 96 (b, h) x 1 query tile: enough splits for 256 workgroups, at least 512 keys each
-    assert [lib.bd3_decode_auto_splits(8, 12, 32, kv) for kv in (100, 544, 1056, 2080, 4096)] == [1, 1, 2, 3, 3]
+    # 96 (b, h) x 1 32-row tile: about 128 workgroups, at least 1024 keys per
+    # split with 64 or more tiles (512 with fewer)
+    assert [lib.bd3_decode_auto_splits(8, 12, 32, kv) for kv in (100, 544, 1056, 2080, 4096)] == [1, 1, 1, 2, 2]
+    assert lib.bd3_decode_auto_splits(1, 12, 32, 3584) == 7
     # a cached step (q_len <= 16): down to 128 keys per split, at most 16 splits
     assert [lib.bd3_decode_auto_splits(1, 12, 16, kv) for kv in (200, 544, 3584, 8192)] == [1, 4, 16, 16]
     assert lib.bd3_decode_auto_splits(2, 12, 16, 1024) == 8
