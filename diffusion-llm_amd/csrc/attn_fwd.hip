@@ -386,29 +386,45 @@ __global__ __launch_bounds__(256, OCC) void prefill_attn_kernel(DecodeArgs a) {
 
 // Merges the split partials of the rows whose 128-row tile spans several
 // splits (the kernel wrote the other rows' O): weights exp2(lse_s - max lse)
-// as in decode_combine, 16 threads per row, 4 outputs each, up to 8 splits
-// per memory round trip. Grid: (32-row tiles, batch*head).
-__global__ __launch_bounds__(256) void prefill_combine(DecodeArgs a) {
+// as in decode_combine; 16 threads per row, 4 outputs each, all 32 rows of a
+// tile in one workgroup. Up to 8 splits (the common case) take one memory
+// round trip: every load is issued before the first use; more splits go 8
+// per round trip. Grid: (32-row tiles, batch*head).
+__global__ __launch_bounds__(512) void prefill_combine(DecodeArgs a) {
   const int qt = wg_x();
   const int bh = wg_y();
   const int i0 = qt * 32;
   const int e = decode_key_end(i0 & ~127, 128, a.q_len, a.kv_len, a.bs);
   const int ns = (e + a.split_len - 1) / a.split_len;
-  if (ns <= 1) return;
+  const int tid = wi_x();
+  const int row = tid >> 4;
+  if (ns <= 1 || i0 + row >= a.q_len) return;
   const int b = bh / a.heads, h = bh - b * a.heads;
   uint16_t* op = a.o + b * a.so.b + h * a.so.h;
   const int64_t slot0 = ((int64_t)bh * a.q_tiles + qt) * a.n_splits;
-  const int tid = wi_x();
   const int d0 = 4 * (tid & 15);
   constexpr int kG = 8;
+  const float* lp = a.part_lse + slot0 * 32 + row;                  // split s: lp[32 s]
+  const float* pp = a.part_o + (slot0 * 32 + row) * kHeadDim + d0;  // split s: pp[32 * 64 s]
+  float mm = -INFINITY, wt = 0.f;
+  f32x4 acc = {};
+  if (ns <= kG) {
+    float l[kG];
+    f32x4 po[kG];
 #pragma unroll
-  for (int pass = 0; pass < 2; ++pass) {
-    const int row = pass * 16 + (tid >> 4);
-    if (i0 + row >= a.q_len) continue;
-    const float* lp = a.part_lse + slot0 * 32 + row;                  // split s: lp[32 s]
-    const float* pp = a.part_o + (slot0 * 32 + row) * kHeadDim + d0;  // split s: pp[32 * 64 s]
-    float mm = -INFINITY, wt = 0.f;
-    f32x4 acc = {};
+    for (int k = 0; k < kG; ++k) {
+      l[k] = k < ns ? lp[k * 32] : -INFINITY;
+      po[k] = k < ns ? *reinterpret_cast<const f32x4*>(pp + k * 32 * kHeadDim) : f32x4{};
+    }
+#pragma unroll
+    for (int k = 0; k < kG; ++k) mm = fmaxf(mm, l[k]);
+#pragma unroll
+    for (int k = 0; k < kG; ++k) {
+      const float w = k < ns ? fast_exp2(l[k] - mm) : 0.f;  // a split the row does not see: 0
+      wt += w;
+      acc += w * po[k];
+    }
+  } else {
     for (int s0 = 0; s0 < ns; s0 += kG) {
       float l[kG];
 #pragma unroll
@@ -429,16 +445,16 @@ __global__ __launch_bounds__(256) void prefill_combine(DecodeArgs a) {
 #pragma unroll
       for (int k = 0; k < kG; ++k) {
         if (s0 + k < ns) {
-          const float w = fast_exp2(l[k] - mm);  // a split the row does not see: 0
+          const float w = fast_exp2(l[k] - mm);
           wt += w;
           acc += w * po[k];
         }
       }
     }
-    const float inv = 1.f / wt;
-    *reinterpret_cast<bf16x4*>(op + (int64_t)(i0 + row) * a.so.s + d0) =
-        to_bf16x4(acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv);
   }
+  const float inv = 1.f / wt;
+  *reinterpret_cast<bf16x4*>(op + (int64_t)(i0 + row) * a.so.s + d0) =
+      to_bf16x4(acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv);
 }
 
 }  // namespace
@@ -469,7 +485,7 @@ hipError_t launch_prefill(const DecodeArgs& a, hipStream_t stream) {
   // The last tile sees the most keys: if they fit one split, no partials.
   if (e != hipSuccess || decode_key_end(128 * (row_tiles - 1), 128, a.q_len, a.kv_len, a.bs) <= a.split_len)
     return e;
-  hipLaunchKernelGGL(prefill_combine, dim3(a.q_tiles, a.bh), block, 0, stream, a);
+  hipLaunchKernelGGL(prefill_combine, dim3(a.q_tiles, a.bh), dim3(512), 0, stream, a);
   return hipGetLastError();
 }
 
