@@ -268,6 +268,51 @@ __global__ __launch_bounds__(256) void gate_residual_ln_modulate_kernel(GlueArgs
   ln_modulate_row<CH>(a, b, s, lane, v, mv, !res_bf16);
 }
 
+// 4 consecutive elements at p: fp32 (16 bytes) or bf16 (8 bytes), the dtype
+// fixed at compile time.
+template <bool F32>
+__device__ __forceinline__ void load4(const void* p, float (&v)[4]) {
+  if constexpr (F32) {
+    const f32x4 t = *reinterpret_cast<const f32x4*>(p);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = t[k];
+  } else {
+    const uint2 t = *reinterpret_cast<const uint2*>(p);
+    v[0] = __uint_as_float(t.x << 16);
+    v[1] = __uint_as_float(t.x & 0xffff0000u);
+    v[2] = __uint_as_float(t.y << 16);
+    v[3] = __uint_as_float(t.y & 0xffff0000u);
+  }
+}
+
+// x + gate * y with an fp32 residual (the result is fp32): 4 elements per
+// thread, so each load of x (16 bytes per lane) covers one contiguous 1 KB
+// per wave, where 8-element chunks (two 16-byte halves 32 bytes apart per
+// lane) split every load across twice the span. GF / YF: gate / y in fp32.
+// Measured at 8 x 2048 x 768: 25.8 -> 23.3 us, bit-identical.
+template <bool GF, bool YF>
+__global__ __launch_bounds__(256) void gate_residual_f32_kernel(GlueArgs a) {
+#pragma clang fp contract(off)  // gate * y rounded before the add, as the eager ops
+  const int64_t e = (int64_t)wg_x() * 256 + wi_x();  // one 4-element chunk
+  const int nch = a.d >> 2;
+  if (e >= (int64_t)a.rows * nch) return;
+  const int row = (int)(e / nch), c = (int)(e - (int64_t)row * nch);
+  const int b = row / a.seq, s = row - b * a.seq;
+  float x[4], g[4], y[4];
+  load4<true>(static_cast<const float*>(a.x) + (int64_t)b * a.sx_b + (int64_t)s * a.sx_s + 4 * c, x);
+  load4<GF>(elem(a.shift, GF, (int64_t)b * a.sm_b + 4 * c), g);  // gate
+  load4<YF>(elem(a.y, YF, (int64_t)b * a.sy_b + (int64_t)s * a.sy_s + 4 * c), y);
+  const bool gy_bf16 = !GF && !YF;
+  f32x4 o;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float gy = g[k] * y[k];
+    if (gy_bf16) gy = rbf(gy);
+    o[k] = x[k] + gy;
+  }
+  *reinterpret_cast<f32x4*>(static_cast<float*>(a.out) + (int64_t)b * a.so_b + (int64_t)s * a.so_s + 4 * c) = o;
+}
+
 __global__ __launch_bounds__(256) void gate_residual_kernel(GlueArgs a) {
 #pragma clang fp contract(off)  // gate * y rounded before the add, as the eager ops
   const int64_t e = (int64_t)wg_x() * 256 + wi_x();  // one 8-element chunk
@@ -330,6 +375,20 @@ hipError_t launch_gate_residual_ln_modulate(const GlueArgs& a, hipStream_t strea
 }
 
 hipError_t launch_gate_residual(const GlueArgs& a, hipStream_t stream) {
+  if (a.x_fp32) {  // fp32 residual and result: 4-element chunks
+    const int64_t n4 = (int64_t)a.rows * (a.d >> 2);
+    if (n4 == 0) return hipSuccess;
+    const dim3 grid((unsigned)((n4 + 255) / 256));
+    if (a.m_fp32 && a.y_fp32)
+      hipLaunchKernelGGL((gate_residual_f32_kernel<true, true>), grid, dim3(256), 0, stream, a);
+    else if (a.m_fp32)
+      hipLaunchKernelGGL((gate_residual_f32_kernel<true, false>), grid, dim3(256), 0, stream, a);
+    else if (a.y_fp32)
+      hipLaunchKernelGGL((gate_residual_f32_kernel<false, true>), grid, dim3(256), 0, stream, a);
+    else
+      hipLaunchKernelGGL((gate_residual_f32_kernel<false, false>), grid, dim3(256), 0, stream, a);
+    return hipGetLastError();
+  }
   const int64_t n = (int64_t)a.rows * (a.d >> 3);
   if (n == 0) return hipSuccess;
   hipLaunchKernelGGL(gate_residual_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, a);
