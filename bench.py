@@ -755,6 +755,16 @@ def main(argv=None) -> int:
     del step
     torch.cuda.empty_cache()
 
+    # The clock the matrix cores hold under load (the 2.5 PFLOP/s peak above
+    # assumes 2.4 GHz): measured right after the timed steps, for context.
+    from perf.harness import shader_clock_ghz
+    sclk = shader_clock_ghz(lib(), device)
+    result["sclk_under_mfma_load"] = sclk
+    if achieved:
+        result["roofline"]["frac_at_measured_sclk"] = achieved / sclk["bf16_peak_tflops"]
+    log(f"shader clock under MFMA load: {sclk['median']:.3f} GHz (min {sclk['min']:.3f}, max {sclk['max']:.3f}) "
+        f"-> bf16 dense peak {sclk['bf16_peak_tflops']:.0f} TFLOP/s")
+
     if not args.no_decode:
         result["decode"] = decode_bench(device, reps=30)
         for r in result["decode"]["rows"]:

@@ -143,5 +143,6 @@ hipError_t launch_gate_residual_ln_modulate(const GlueArgs& a, hipStream_t strea
 hipError_t launch_gate_residual(const GlueArgs& a, hipStream_t stream);
 hipError_t launch_mask_dump(uint8_t* out, int mode, int rows, int kv_len,
                             int bs, hipStream_t stream);
+hipError_t launch_clock_probe(uint64_t* out, int workgroups, int iters, hipStream_t stream);
 
 }  // namespace bd3

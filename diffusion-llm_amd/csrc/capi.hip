@@ -687,6 +687,20 @@ int bd3_mask_dump(uint8_t* out, int32_t mode, int32_t rows, int32_t kv_len, int3
                     "mask_dump launch");
 }
 
+int bd3_clock_probe(uint64_t* out, int32_t workgroups, int32_t iters, int64_t* wall_rate_khz,
+                    void* stream) {
+  if (out == nullptr || wall_rate_khz == nullptr) return fail(BD3_EINVAL, "out / wall_rate_khz is NULL");
+  if (workgroups < 1 || workgroups > 65536) return fail(BD3_EINVAL, "workgroups must be in [1, 65536]");
+  if (iters < 1) return fail(BD3_EINVAL, "iters must be >= 1");
+  int dev = 0, rate = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&rate, hipDeviceAttributeWallClockRate, dev);
+  if (e != hipSuccess) return hip_status(e, "wall clock rate query");
+  *wall_rate_khz = rate;
+  return hip_status(bd3::launch_clock_probe(out, workgroups, iters, static_cast<hipStream_t>(stream)),
+                    "clock_probe launch");
+}
+
 int bd3_train_classify(int32_t n, int32_t block_size, int32_t q0, int32_t k0) {
   if (n < 32 || n % 32 != 0 || block_size < 1) return -1;
   if (q0 < 0 || k0 < 0 || q0 + 32 > 2 * n || k0 + 32 > 2 * n || q0 % 32 || k0 % 32) return -1;

@@ -58,6 +58,7 @@ SIGNATURES: dict[str, tuple] = {
                                                      _i32, _c_p, _i32, _i32, _i32, _i32, _i64p, _f32,
                                                      _c_p]),
     "bd3_mask_dump": (ctypes.c_int, [_c_p, _i32, _i32, _i32, _i32, _c_p]),
+    "bd3_clock_probe": (ctypes.c_int, [_c_p, _i32, _i32, _i64p, _c_p]),
     "bd3_train_tile_census": (ctypes.c_int, [_i32, _i32, _i64p]),
     "bd3_train_classify": (ctypes.c_int, [_i32, _i32, _i32, _i32]),
     "bd3_train_classify_keys": (ctypes.c_int, [_i32, _i32, _i32, _i32]),

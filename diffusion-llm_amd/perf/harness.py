@@ -185,3 +185,28 @@ def time_calls(fn: Callable[[], Any], reps: int = 30, warmup: int = 5, flush: bo
 def bench(fn: Callable[[], Any], warmup: int = 5, rep: int = 30, flush: bool = True) -> Samples:
     """time_calls with the argument names the bench sections use."""
     return time_calls(fn, reps=rep, warmup=warmup, flush=flush)
+
+
+def shader_clock_ghz(lib: ctypes.CDLL, device: torch.device, workgroups: int = 1024,
+                     iters: int = 40000) -> dict:
+    """The shader clock the chip holds under a full matrix-core load, from
+    `bd3_clock_probe` (every SIMD busy with independent bf16 MFMA chains for
+    ~10 ms): per workgroup, shader-clock ticks over constant-rate real-time
+    ticks times the real-time rate. Returns the median and extremes over the
+    workgroups in GHz, and the bf16 dense peak that clock gives (256 CUs x
+    4096 FLOP per clock)."""
+    out = torch.zeros(2 * workgroups, dtype=torch.int64, device=device)
+    rate = ctypes.c_int64(0)
+    stream = ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+    for _ in range(2):  # the first launch settles the clock; the second is read
+        rc = lib.bd3_clock_probe(ctypes.c_void_p(out.data_ptr()), workgroups, iters, ctypes.byref(rate), stream)
+        if rc != 0:
+            raise RuntimeError(f"bd3_clock_probe failed: {lib.bd3_last_error().decode()}")
+    torch.cuda.synchronize(device)
+    t = out.view(workgroups, 2).double().cpu()
+    ghz = (t[:, 0] / t[:, 1] * rate.value / 1e6).tolist()
+    ghz.sort()
+    med = ghz[len(ghz) // 2]
+    return {"median": med, "min": ghz[0], "max": ghz[-1], "wall_rate_khz": rate.value,
+            "bf16_peak_tflops": 256 * 4096 * med * 1e9 / 1e12,
+            "probe": f"{workgroups} workgroups x 4 waves, {iters} rounds of 4 independent 32x32x16 bf16 MFMAs"}

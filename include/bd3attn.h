@@ -354,6 +354,22 @@ int bd3_mask_dump(uint8_t* out, int32_t mode, int32_t rows, int32_t kv_len,
                   int32_t block_size, void* stream);
 
 /*
+ * Measurement aid, no reference counterpart: the shader clock under a
+ * matrix-core load, for pricing kernels against the clock the chip holds
+ * rather than the datasheet's 2.4 GHz. Launches `workgroups` workgroups of
+ * 256 threads that each run `iters` rounds of four independent bf16 MFMA
+ * chains per wave (no memory reads). Workgroup i writes out[2i] = shader
+ * clock ticks (s_memtime) and out[2i+1] = constant-rate real-time ticks
+ * (s_memrealtime) elapsed over its loop; *wall_rate_khz receives the
+ * real-time counter's rate (hipDeviceAttributeWallClockRate), so the clock
+ * is out[2i] / out[2i+1] * wall_rate_khz kHz.
+ * Preconditions: out holds 2 * workgroups uint64; 1 <= workgroups <= 65536;
+ * iters >= 1.
+ */
+int bd3_clock_probe(uint64_t* out, int32_t workgroups, int32_t iters, int64_t* wall_rate_khz,
+                    void* stream);
+
+/*
  * Host-only (no GPU needed): tile census of the training-attention
  * schedules for one (batch, head). Writes out[0..7] =
  *   {useful pairs,

@@ -224,6 +224,15 @@ def test_decode_validation(lib):
     expect_einval(lib.bd3_mask_dump(GOOD, 1, 5, 4, 1, None), "q_len")
 
 
+def test_clock_probe_validation(lib):
+    rate = ctypes.c_int64(0)
+    expect_einval(lib.bd3_clock_probe(None, 4, 10, ctypes.byref(rate), None), "NULL")
+    expect_einval(lib.bd3_clock_probe(GOOD, 0, 10, ctypes.byref(rate), None), "workgroups")
+    expect_einval(lib.bd3_clock_probe(GOOD, 65537, 10, ctypes.byref(rate), None), "workgroups")
+    expect_einval(lib.bd3_clock_probe(GOOD, 4, 0, ctypes.byref(rate), None), "iters")
+    expect_einval(lib.bd3_clock_probe(GOOD, 4, 10, None, None), "NULL")
+
+
 def test_workspace_sizes(lib):
     # one split needs no workspace; partials are (BH, q_tiles, splits, 32, 64) fp32 + LSE
     assert lib.bd3_decode_workspace_bytes(2, 3, 16, 100, 64, 1) == 0
