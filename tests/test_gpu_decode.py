@@ -9,6 +9,7 @@ import torch
 from _gpu_util import max_abs, splitkv_capi
 from kernels.BlockSparseDecodeAttention import block_sparse_decode_attention
 from kernels.SplitKVDecodeAttention import split_kv_decode_attention
+from kernels._native import check, lib, ptr, stream_of, strides
 from oracle.attention import bf16_round, decode_attention, seeded_normal
 
 OUT_TOL = 2e-2
@@ -189,3 +190,24 @@ def test_batch1_profiling_shapes(cuda, record_error, shape, backend):
     ref = decode_attention(q, k, v, 16)
     torch.cuda.synchronize()
     record_error("decode O max-abs", max_abs(o, ref), OUT_TOL)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("q_len,kv_len,n_splits", [(1, 300, 1), (16, 700, 1), (16, 700, 3), (32, 1000, 2),
+                                                   (300, 1100, 1), (300, 1100, 3)])
+def test_decode_scale_argument(cuda, q_len, kv_len, n_splits):
+    """`scale` is applied, not assumed, on every decode path (q_len 1-16,
+    17-64, the prefill kernel above 64; one split and merged splits):
+    doubling q and halving scale leaves the logits, hence O, bit-identical."""
+    B, H, bs = 2, 3, 16
+    q, k, v = (t.to(cuda, torch.bfloat16) for t in decode_inputs(B, H, q_len, kv_len, seed=q_len + kv_len))
+    outs = []
+    for qq, scale in ((q, 0.125), (q * 2, 0.0625)):
+        o = torch.empty_like(qq)
+        nbytes = lib().bd3_decode_workspace_bytes(B, H, q_len, kv_len, 64, n_splits)
+        ws = torch.empty(max(nbytes, 1), device=cuda, dtype=torch.uint8)
+        check(lib().bd3_decode_splitkv(ptr(qq), ptr(k), ptr(v), ptr(o), B, H, q_len, kv_len, 64, bs, n_splits,
+                                       strides(qq, k, v, o), scale, ptr(ws), nbytes, stream_of(qq)))
+        outs.append(o)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])

@@ -8,6 +8,7 @@ import pytest
 import torch
 
 from _gpu_util import bwd_capi, fwd_capi, max_abs, to_dev, train_inputs
+from kernels._native import check, lib, ptr, stream_of, strides
 from kernels.BlockSparseFlashAttention import BlockSparseFlashAttention
 from oracle.attention import bd3_attention, bd3_attention_grads, bd3_attention_grads_rows, rel_frobenius
 
@@ -149,3 +150,70 @@ def test_strided_v_read_in_place(cuda):
     o2, l2 = fwd_capi(q.contiguous(), k.contiguous(), v.contiguous(), bs)
     torch.cuda.synchronize()
     assert torch.equal(o1, o2) and torch.equal(l1, l2)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("bs", [16, 8])
+def test_strided_backward_in_place(cuda, bs):
+    """The backward reads q, k, v from a fused (B, S, 3, H, d) projection, O and
+    dO from (B, S, H, d) buffers, and writes dQ, dK, dV into three of the four
+    slots of a (B, S, 4, H, d) gradient buffer, all in place through their
+    strides: the gradients equal those of contiguous copies bit for bit, and
+    the fourth slot, between the destinations' rows, stays untouched."""
+    B, H, n = 2, 3, 128
+    g = torch.Generator(device="cpu").manual_seed(11)
+    qkv = torch.randn(B, 2 * n, 3, H, 64, generator=g).to(cuda, torch.bfloat16)
+    do_bshd = torch.randn(B, 2 * n, H, 64, generator=g).to(cuda, torch.bfloat16)
+    q, k, v = (qkv[:, :, i].permute(0, 2, 1, 3) for i in range(3))
+    dout = do_bshd.permute(0, 2, 1, 3)
+    o = torch.empty(B, 2 * n, H, 64, device=cuda, dtype=torch.bfloat16).permute(0, 2, 1, 3)
+    lse = torch.empty(B, H, 2 * n, device=cuda, dtype=torch.float32)
+    check(lib().bd3_attn_fwd(ptr(q), ptr(k), ptr(v), ptr(o), ptr(lse), B, H, n, 64, bs, strides(q, k, v, o),
+                             0.125, stream_of(q)))
+    sentinel = -3.0
+    dbuf = torch.full((B, 2 * n, 4, H, 64), sentinel, device=cuda, dtype=torch.bfloat16)
+    dq, dk, dv = (dbuf[:, :, i].permute(0, 2, 1, 3) for i in range(3))
+    nbytes = lib().bd3_attn_bwd_workspace_bytes(B, H, n, 64)
+    ws = torch.empty(nbytes, device=cuda, dtype=torch.uint8)
+    check(lib().bd3_attn_bwd(ptr(q), ptr(k), ptr(v), ptr(o), ptr(dout), ptr(lse), ptr(dq), ptr(dk), ptr(dv),
+                             ptr(ws), nbytes, B, H, n, 64, bs, strides(q, k, v, o, dout, dq, dk, dv), 0.125,
+                             stream_of(q)))
+    qc, kc, vc, doc = (t.contiguous() for t in (q, k, v, dout))
+    o2, lse2 = fwd_capi(qc, kc, vc, bs)
+    dq2, dk2, dv2 = bwd_capi(qc, kc, vc, o2, doc, lse2, bs)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o2) and torch.equal(lse, lse2)
+    for a, b in ((dq, dq2), (dk, dk2), (dv, dv2)):
+        assert torch.equal(a, b)
+    assert bool((dbuf[:, :, 3] == sentinel).all()), "a write landed outside the gradient views"
+
+
+@pytest.mark.gpu
+def test_scale_argument(cuda):
+    """`scale` is applied, not assumed: doubling q and halving scale leaves
+    the logits unchanged, so O, lse, dK and dV are bit-identical and dQ is
+    exactly halved (power-of-two factors are exact in bf16 and fp32)."""
+    B, H, n, bs = 1, 2, 256, 16
+    q, k, v, do = to_dev(train_inputs(B, H, n, seed=5, count=4), cuda)
+    q2 = q * 2
+
+    def run(qq, scale):
+        S = qq.shape[2]
+        o = torch.empty_like(qq)
+        lse = torch.empty((B, H, S), device=cuda, dtype=torch.float32)
+        check(lib().bd3_attn_fwd(ptr(qq), ptr(k), ptr(v), ptr(o), ptr(lse), B, H, n, 64, bs,
+                                 strides(qq, k, v, o), scale, stream_of(qq)))
+        grads = [torch.empty_like(qq) for _ in range(3)]
+        nbytes = lib().bd3_attn_bwd_workspace_bytes(B, H, n, 64)
+        ws = torch.empty(nbytes, device=cuda, dtype=torch.uint8)
+        check(lib().bd3_attn_bwd(ptr(qq), ptr(k), ptr(v), ptr(o), ptr(do), ptr(lse), *(ptr(g) for g in grads),
+                                 ptr(ws), nbytes, B, H, n, 64, bs, strides(qq, k, v, o, do, *grads), scale,
+                                 stream_of(qq)))
+        return o, lse, grads
+
+    o1, l1, (dq1, dk1, dv1) = run(q, 0.125)
+    o2, l2, (dq2, dk2, dv2) = run(q2, 0.0625)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)
+    assert torch.equal(dk1, dk2) and torch.equal(dv1, dv2)
+    assert torch.equal(dq2 * 2, dq1)
