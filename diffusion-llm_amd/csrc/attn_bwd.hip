@@ -17,11 +17,11 @@
 //   L and Delta are per-lane scalars; dQ^T += K^T dS^T reads K^T from the LDS
 //   tile with ds_read_b64_tr_b16. Delta = rowsum(dO o O) is formed here from
 //   the row registers and stored for the second kernel (this fuses the
-//   reference's separate Delta op), next to the rows' L * log2(e), so the
-//   second kernel's exponent is one fma per element.
+//   reference's separate Delta op), next to the rows' -L / scale, the
+//   second kernel's score-chain seed.
 // attn_bwd_dkdv_dma_kernel (key-stationary): 4 waves of 32 keys. K and V rows
 //   live in registers as B operands of S = Q K^T and dP = dO V^T, which put
-//   one key per lane; query tiles (Q, dO, L * log2(e), Delta) come through LDS.
+//   one key per lane; query tiles (Q, dO, -L / scale, Delta) come through LDS.
 //   dV += P^T dO and dK += dS^T Q take P^T / dS^T straight from registers and
 //   dO / Q transposed from LDS. dK, dV are written through LDS as 16-byte rows.
 // Both load their tiles global -> LDS with global_load_lds into three-stage
@@ -47,7 +47,7 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dkdv_dma_kernel(BwdArgs a) 
   constexpr int kBK = 128;  // keys per workgroup: 4 waves x 32
   constexpr int kStages = 3;
   // Stage layout (bytes): Q tile [0, 8K), dO tile [8K, 16K), row scalars
-  // [16K, 17K): L * log2(e) of the 64 rows, then Delta, then both again (the
+  // [16K, 17K): -L / scale of the 64 rows, then Delta, then both again (the
   // load that fetches them writes 1 KB).
   constexpr int kStageBytes = 4 * kSwTile + 1024;
   __shared__ __attribute__((aligned(1024))) __bf16 smem[kStages * kStageBytes / 2];
@@ -95,7 +95,7 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dkdv_dma_kernel(BwdArgs a) 
     qoff[j] = (uint32_t)(2 * (r * (int)a.sq.s + ch));
     dooff[j] = (uint32_t)(2 * (r * (int)a.sdo.s + ch));
   }
-  // L comes as L * log2(e), the second plane of the delta buffer (written by the dQ kernel).
+  // L comes as -L / scale, the second plane of the delta buffer (written by the dQ kernel).
   const float* scal_src = ((lane & 16) ? a.delta : a.delta + (int64_t)a.bh * 2 * a.n) + rowbase + 4 * (lane & 15);
   const int64_t qstep = (int64_t)kSwRows * a.sq.s, dostep = (int64_t)kSwRows * a.sdo.s;
   const uint32_t lds0 = lds_addr(&smem[0]);
@@ -134,11 +134,8 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dkdv_dma_kernel(BwdArgs a) 
 #pragma unroll
   for (int c = 0; c < 4; ++c)
     vreg[c] = __builtin_bit_cast(bf16x8, __builtin_bit_cast(u32x4, vreg[c]) ^ 0x80008000u);
-  // K is held times -scale * log2(e) (rounded to bf16) and the score chains
-  // start from the rows' L * log2(e), so they give minus the base-2 exponent
-  // of P (negated for free by the exp's input modifier).
-#pragma unroll
-  for (int c = 0; c < 4; ++c) kreg[c] = scale_bf16x8(kreg[c], -a.scale_log2);
+  // The score chains start from the rows' -L / scale, so they give the
+  // exact fp32 S - L / scale; P = exp2 of that times scale * log2(e).
 #pragma unroll
   for (int c = 0; c < 4; ++c) asm volatile("" ::"v"(kreg[c]), "v"(vreg[c]));
   const RowIntervals civ = train_col_intervals(key, a.n, a.bs);
@@ -148,7 +145,7 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dkdv_dma_kernel(BwdArgs a) 
 
   // Scores and Delta - dP of the 32-row blocks of the current query tile
   // (rows x keys, lane = key column, register r <-> row 32qb + 8(r/4) + 4g +
-  // r%4): the chains start from the rows' L * log2(e) and Delta, read from the
+  // r%4): the chains start from the rows' -L / scale and Delta, read from the
   // tile's row scalars in accumulator order. The two blocks' four chains are
   // issued interleaved, so no product waits for the one before it.
   auto products = [&](const __bf16* qs, const __bf16* dos, const float* scal, f32x16 (&s)[2], f32x16 (&dp)[2]) {
@@ -168,12 +165,12 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dkdv_dma_kernel(BwdArgs a) 
     for (int c = 0; c < 4; ++c)
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
-        s[qb] = mfma32(sw_row_op(qs, 32 * qb, c, lane), kreg[c], s[qb]);     // L log2(e) - S scale log2(e)
+        s[qb] = mfma32(sw_row_op(qs, 32 * qb, c, lane), kreg[c], s[qb]);     // S - L / scale
         dp[qb] = mfma32(sw_row_op(dos, 32 * qb, c, lane), vreg[c], dp[qb]);  // Delta - dP (V negated)
       }
   };
 
-  // P^T and -dS^T operands of block qb: P = exp2(-s), -dS = P o (Delta -
+  // P^T and -dS^T operands of block qb: P = exp2(s * scale * log2(e)), -dS = P o (Delta -
   // dP). A block that is not fully visible gets P = 0 on its invisible
   // pairs: with MASK16 (block size a multiple of 16) the mask is constant on
   // 16-row x 1-key strips, so one test per lane for rows 0-15 of the block
@@ -183,7 +180,7 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dkdv_dma_kernel(BwdArgs a) 
                          bf16x8 (&dsop)[2]) {
     float p[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) p[r] = fast_exp2(-s[r]);
+    for (int r = 0; r < 16; ++r) p[r] = fast_exp2(s[r] * a.scale_log2);
     if (masked) {
       if (MASK16) {
         const bool lo = iv_has(civ, q0 + 32 * qb), hi = iv_has(civ, q0 + 32 * qb + 16);
@@ -362,9 +359,10 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dq_dma_kernel(BwdArgs a) {
     for (int j = 0; j < 8; ++j) dsum = fmaf((float)doreg[c][j], (float)oreg[c][j], dsum);
   const float drow = sum_xor32(dsum);
   const float lrow = lse_row * kLog2e;
+  const float lseed = -lse_row / a.scale;
   if (g == 0) {
     a.delta[rowbase + myq] = drow;
-    a.delta[(int64_t)a.bh * 2 * a.n + rowbase + myq] = lrow;  // second plane: L * log2(e) for dK/dV
+    a.delta[(int64_t)a.bh * 2 * a.n + rowbase + myq] = lseed;  // second plane: -L / scale for dK/dV
   }
 #pragma unroll
   for (int c = 0; c < 4; ++c) asm volatile("" ::"v"(qreg[c]), "v"(doreg[c]));

@@ -181,10 +181,8 @@ __device__ __forceinline__ void fwd_body(Args a) {
 #pragma unroll
   for (int i = 0; i < kAhead; ++i)
     if (i < n_tiles) issue(i);
-  // Q times scale * log2(e), rounded to bf16: K Q'^T is then the base-2
-  // exponent, and a chain started from -m gives S * scale * log2(e) - m.
 #pragma unroll
-  for (int c = 0; c < 4; ++c) qreg[c] = scale_bf16x8(qreg[c], a.scale_log2);
+  for (int c = 0; c < 4; ++c) asm volatile("" ::"v"(qreg[c]));
   RowIntervals riv;
   WalkClasses wc;
   if constexpr (PREFILL) {
@@ -211,11 +209,12 @@ __device__ __forceinline__ void fwd_body(Args a) {
   }
 
   f32x16 o[2] = {};  // O^T [d block]
-  // mref: the row's reference maximum (log2 units); the score chains start
-  // from negm = -mref. `valid` once the row has met a live key.
+  // mref: the row's reference maximum (log2 units); `valid` once the row
+  // has met a live key. Scores are exact fp32 dot products of the bf16 rows;
+  // scale * log2(e) is applied to each one in the exponent's FMA.
   float mref = 0.f, lsum = 0.f;
   bool valid = false;
-  f32x16 negm = {};
+  const float c2 = a.scale_log2;
 
   // One tile step over NSB 32-key halves of the current 64-key tile,
   // starting at half sb0 (NSB = 1: the other half is dead for this wave).
@@ -228,7 +227,7 @@ __device__ __forceinline__ void fwd_body(Args a) {
       for (int c = 0; c < 4; ++c) kop[sb][c] = sw_row_op(ks, 32 * (sb0 + sb), c, lane);
     f32x16 s[NSB];
 #pragma unroll
-    for (int sb = 0; sb < NSB; ++sb) s[sb] = mfma32(kop[sb][0], qreg[0], negm);
+    for (int sb = 0; sb < NSB; ++sb) s[sb] = mfma32(kop[sb][0], qreg[0], f32x16{});
 #pragma unroll
     for (int c = 1; c < 4; ++c)
 #pragma unroll
@@ -255,7 +254,8 @@ __device__ __forceinline__ void fwd_body(Args a) {
         }
       }
     }
-    // Row max of the shifted scores: four independent v_max3 chains.
+    // Row max of the scores: four independent v_max3 chains, then scaled to
+    // the base-2 exponent relative to the current reference.
     float mq[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -267,20 +267,15 @@ __device__ __forceinline__ void fwd_body(Args a) {
         mq[q] = fmaxf(fmaxf(mq[q], s[sb][4 * q + 2]), s[sb][4 * q + 3]);
       }
     }
-    const float mt = max_xor32(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3])));
+    const float mt = fmaf(max_xor32(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]))), c2, -mref);
     // A new reference when the row had none (and this tile has a live key)
-    // or its maximum grew by more than kRescale: the scores shift by delta,
-    // O and l scale by 2^-delta.
+    // or its maximum grew by more than kRescale: the reference rises by
+    // delta, O and l scale by 2^-delta.
     if (__ballot(!valid || mt > kRescale) != 0) {
       const float delta = valid ? fmaxf(mt, 0.f) : (mt == -INFINITY ? 0.f : mt);
       const float alpha = valid ? fast_exp2(-delta) : 1.f;
       valid = valid || mt != -INFINITY;
       mref += delta;
-      negm = splat16(-mref);
-#pragma unroll
-      for (int sb = 0; sb < NSB; ++sb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[sb][r] -= delta;
       lsum *= alpha;
       o[0] *= alpha;
       o[1] *= alpha;
@@ -290,12 +285,14 @@ __device__ __forceinline__ void fwd_body(Args a) {
     for (int sb = 0; sb < NSB; ++sb) {
       float p[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) p[r] = fast_exp2(s[sb][r]);
+      for (int r = 0; r < 16; ++r) p[r] = fast_exp2(fmaf(s[sb][r], c2, -mref));
+      // The row sum in fp32 from the unrounded P, as the reference's l.
 #pragma unroll
       for (int kc = 0; kc < 2; ++kc) {
         pop[sb][kc] = to_bf16x8(p[8 * kc], p[8 * kc + 1], p[8 * kc + 2], p[8 * kc + 3], p[8 * kc + 4],
                                 p[8 * kc + 5], p[8 * kc + 6], p[8 * kc + 7]);
-        lsum = sum_bf16x8(pop[sb][kc], lsum);
+        lsum += ((p[8 * kc] + p[8 * kc + 1]) + (p[8 * kc + 2] + p[8 * kc + 3])) +
+                ((p[8 * kc + 4] + p[8 * kc + 5]) + (p[8 * kc + 6] + p[8 * kc + 7]));
       }
     }
 #pragma unroll

@@ -35,18 +35,6 @@ __device__ __forceinline__ WalkClasses uniform_walk(WalkClasses w) {
   return w;
 }
 
-// Sum of the 8 bf16 values of a P operand added to acc, as 4 v_dot2c_f32_bf16
-// against (1, 1): the softmax denominator accumulates exactly the rounded
-// probabilities the PV product uses, at half the VALU cost of fp32 adds.
-__device__ __forceinline__ float sum_bf16x8(bf16x8 v, float acc) {
-  const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
-  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 0, 1), one, acc, false);
-  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 2, 3), one, acc, false);
-  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 4, 5), one, acc, false);
-  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 6, 7), one, acc, false);
-  return acc;
-}
-
 // Visibility of key k for a row with intervals iv, as 0/1 without branches.
 __device__ __forceinline__ bool iv_has(const RowIntervals& iv, int k) {
   return ((unsigned)(k - iv.lo1) < (unsigned)(iv.hi1 - iv.lo1)) |

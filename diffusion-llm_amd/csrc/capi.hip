@@ -5,6 +5,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <cmath>
 #include <mutex>
 #include <string>
 
@@ -82,6 +83,14 @@ int check_common_decode(const void* q, const void* k, const void* v, void* o, in
     int st = check_tensor(ptrs[i], strides + 3 * i, names[i]);
     if (st) return st;
   }
+  return BD3_OK;
+}
+
+// The kernels take a row's maximum over the raw scores and scale it
+// afterwards, which needs scale > 0 (the reference's is 1 / sqrt(head_dim)).
+int check_scale(float scale) {
+  if (!(scale > 0.f) || !std::isfinite(scale))
+    return fail(BD3_EINVAL, "scale must be finite and > 0, got %g", (double)scale);
   return BD3_OK;
 }
 
@@ -182,6 +191,7 @@ int run_decode(const void* q, const void* k, const void* v, void* o, int32_t bat
                int32_t heads, int32_t q_len, int32_t kv_len, int32_t block_size,
                int32_t n_splits, const int64_t* strides, float scale, void* workspace,
                size_t workspace_bytes, void* stream) {
+  if (int st = check_scale(scale)) return st;
   const int q_tiles = decode_q_tiles(q_len);
   const size_t need = bd3_decode_workspace_bytes(batch, heads, q_len, kv_len, bd3::kHeadDim, n_splits);
   if (workspace_bytes < need)
@@ -275,6 +285,7 @@ int bd3_attn_fwd(const void* q, const void* k, const void* v, void* o, float* ls
     if (st) return st;
   }
   if (lse == nullptr) return fail(BD3_EINVAL, "lse is NULL");
+  if (int st = check_scale(scale)) return st;
   bd3::FwdArgs a;
   a.q = static_cast<const uint16_t*>(q);
   a.k = static_cast<const uint16_t*>(k);
@@ -295,7 +306,7 @@ int bd3_attn_fwd(const void* q, const void* k, const void* v, void* o, float* ls
 
 size_t bd3_attn_bwd_workspace_bytes(int32_t batch, int32_t heads, int32_t n, int32_t head_dim) {
   if (batch < 1 || heads < 1 || n < 1 || head_dim < 1) return 0;
-  return align256(2 * (size_t)batch * heads * 2 * n * sizeof(float));  // Delta, L * log2(e)
+  return align256(2 * (size_t)batch * heads * 2 * n * sizeof(float));  // Delta, -L / scale
 }
 
 int bd3_attn_bwd_dq(const void* q, const void* k, const void* v, const void* o, const void* dout,
@@ -304,6 +315,7 @@ int bd3_attn_bwd_dq(const void* q, const void* k, const void* v, const void* o, 
                     void* stream) {
   int st = check_bwd_shape(batch, heads, n, head_dim, block_size, strides);
   if (st) return st;
+  if ((st = check_scale(scale))) return st;
   const char* names[6] = {"q", "k", "v", "o", "dout", "dq"};
   const void* ptrs[6] = {q, k, v, o, dout, dq};
   for (int i = 0; i < 6; ++i)
@@ -328,6 +340,7 @@ int bd3_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* d
                       void* stream) {
   int st = check_bwd_shape(batch, heads, n, head_dim, block_size, strides);
   if (st) return st;
+  if ((st = check_scale(scale))) return st;
   const char* names[6] = {"q", "k", "v", "dout", "dk", "dv"};
   const void* ptrs[6] = {q, k, v, dout, dk, dv};
   for (int i = 0; i < 6; ++i)
@@ -354,6 +367,7 @@ int bd3_attn_bwd(const void* q, const void* k, const void* v, const void* o, con
                  void* stream) {
   int st = check_bwd_shape(batch, heads, n, head_dim, block_size, strides);
   if (st) return st;
+  if ((st = check_scale(scale))) return st;
   const char* names[8] = {"q", "k", "v", "o", "dout", "dq", "dk", "dv"};
   const void* ptrs[8] = {q, k, v, o, dout, dq, dk, dv};
   for (int i = 0; i < 8; ++i)
@@ -380,7 +394,7 @@ int bd3_attn_bwd(const void* q, const void* k, const void* v, const void* o, con
 
 // ---------------------------------------------------------------------------
 // Backward without a caller workspace (bd3_attn_bwd_noalloc): the Delta and
-// L * log2(e) planes live in `scratch`, a device array of this library that
+// -L / scale planes live in `scratch`, a device array of this library that
 // each GPU holds from the library's first use on it until the process ends.
 // Host code never passes the array's name to a kernel (on the host it is a
 // stand-in, not a device address): the address each device gives
@@ -425,6 +439,7 @@ int bd3_attn_bwd_noalloc(const void* q, const void* k, const void* v, const void
                          void* stream) {
   int st = check_bwd_shape(batch, heads, n, head_dim, block_size, strides);
   if (st) return st;
+  if ((st = check_scale(scale))) return st;
   const size_t need = bd3_attn_bwd_workspace_bytes(batch, heads, n, head_dim);
   if (need > kScratchBytes)
     return fail(BD3_EINVAL,

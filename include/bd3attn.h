@@ -24,6 +24,9 @@
  *     message describing the last failure on the calling thread.
  *   - head_dim must be 64 (the reference's only configuration: d_model
  *     768 / 12 heads).
+ *   - The attention entry points take the softmax scale (the reference
+ *     passes 1 / sqrt(head_dim)); it must be finite and > 0. Scores are
+ *     the exact fp32 dot products of the bf16 rows, scaled in fp32.
  *
  * Reentrant: no mutable global state besides the thread-local error
  * message.
@@ -70,7 +73,7 @@ int bd3_attn_fwd(const void* q, const void* k, const void* v, void* o,
 
 /*
  * Bytes of workspace bd3_attn_bwd needs: two fp32 (batch, heads, 2n)
- * planes, Delta = rowsum(dO * O) and L * log2(e). No reference counterpart
+ * planes, Delta = rowsum(dO * O) and -L / scale. No reference counterpart
  * (the reference allocates Delta with a torch op,
  * kernels/BlockSparseFlashAttention.py:525).
  */
@@ -80,7 +83,7 @@ size_t bd3_attn_bwd_workspace_bytes(int32_t batch, int32_t heads, int32_t n,
 /*
  * Training attention backward: dQ, dK, dV of the forward above, given
  * dO and the forward's O and lse. Runs bd3_attn_bwd_dq then
- * bd3_attn_bwd_dkdv with Delta and L * log2(e) in the workspace.
+ * bd3_attn_bwd_dkdv with Delta and -L / scale in the workspace.
  * strides: 24 int64 = (b, h, s) element strides of
  *          q, k, v, o, dout, dq, dk, dv.
  * Preconditions: as the forward, plus n % block_size == 0 (the reference
@@ -98,7 +101,7 @@ int bd3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
 
 /*
  * bd3_attn_bwd without a workspace argument: the same kernels and results
- * (bit for bit), with the Delta and L * log2(e) planes kept in a fixed
+ * (bit for bit), with the Delta and -L / scale planes kept in a fixed
  * device array inside the library (8 MiB per GPU, held from the library's
  * first call of this function on that GPU until the process ends).
  * No counterpart in the reference: for callers that cannot allocate device
@@ -120,9 +123,9 @@ int bd3_attn_bwd_noalloc(const void* q, const void* k, const void* v,
 
 /*
  * Backward, first stage: dQ = scale * dS K with dS = P o (dP - Delta),
- * and, for the second stage, Delta = rowsum(dO * O) and the forward's L
- * times log2(e) written to `delta`: fp32, contiguous (2, batch, heads, 2n),
- * plane 0 Delta, plane 1 L * log2(e).
+ * and, for the second stage, Delta = rowsum(dO * O) and minus the
+ * forward's L over scale written to `delta`: fp32, contiguous (2, batch,
+ * heads, 2n), plane 0 Delta, plane 1 -L / scale.
  * strides: 18 int64 = (b, h, s) element strides of q, k, v, o, dout, dq.
  * Preconditions: as bd3_attn_bwd.
  *
@@ -137,8 +140,8 @@ int bd3_attn_bwd_dq(const void* q, const void* k, const void* v,
 
 /*
  * Backward, second stage: dV = P^T dO and dK = scale * dS^T Q, given the
- * two planes (Delta, L * log2(e)) the first stage wrote to `delta`; `lse`
- * is checked but not read (the kernel uses its base-2 copy).
+ * two planes (Delta, -L / scale) the first stage wrote to `delta`; `lse`
+ * is checked but not read (the kernel uses the plane).
  * strides: 18 int64 = (b, h, s) element strides of q, k, v, dout, dk, dv.
  * Preconditions: as bd3_attn_bwd.
  *

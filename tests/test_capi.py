@@ -165,7 +165,7 @@ def test_fwd_validation(lib):
 def test_bwd_validation(lib):
     st = _i64([64 * 256, 64 * 256, 64] * 8)
     need = lib.bd3_attn_bwd_workspace_bytes(1, 1, 128, 64)
-    assert need == 2 * 1 * 1 * 256 * 4  # Delta and L * log2(e)
+    assert need == 2 * 1 * 1 * 256 * 4  # Delta and -L / scale
     args = [GOOD] * 9
     expect_einval(lib.bd3_attn_bwd(*args, GOOD, need, 1, 1, 128, 64, 3, st, 0.125, None), "multiple of block_size")
     expect_einval(lib.bd3_attn_bwd(*args, GOOD, need - 1, 1, 1, 128, 64, 16, st, 0.125, None), "workspace")
@@ -175,6 +175,27 @@ def test_bwd_validation(lib):
     expect_einval(lib.bd3_attn_bwd_dkdv(*[GOOD] * 8, 1, 1, 128, 64, 5, st18, 0.125, None), "block_size")
     expect_einval(lib.bd3_attn_bwd_dkdv(GOOD, GOOD, GOOD, GOOD + 8, *[GOOD] * 4, 1, 1, 128, 64, 16, st18,
                                         0.125, None), "dout")
+
+
+@pytest.mark.parametrize("scale", [0.0, -0.125, float("nan"), float("inf")])
+def test_scale_validation(lib, scale):
+    """The kernels take row maxima over the raw scores and scale them
+    afterwards: every attention entry point rejects a scale that is not
+    finite and positive."""
+    st = _i64([64 * 256, 64 * 256, 64] * 4)
+    expect_einval(lib.bd3_attn_fwd(GOOD, GOOD, GOOD, GOOD, GOOD, 1, 1, 128, 64, 16, st, scale, None), "scale")
+    st24 = _i64([64 * 256, 64 * 256, 64] * 8)
+    need = lib.bd3_attn_bwd_workspace_bytes(1, 1, 128, 64)
+    expect_einval(lib.bd3_attn_bwd(*[GOOD] * 9, GOOD, need, 1, 1, 128, 64, 16, st24, scale, None), "scale")
+    expect_einval(lib.bd3_attn_bwd_noalloc(*[GOOD] * 9, 1, 1, 128, 64, 16, st24, scale, None), "scale")
+    st18 = _i64([64 * 256, 64 * 256, 64] * 6)
+    expect_einval(lib.bd3_attn_bwd_dq(*[GOOD] * 8, 1, 1, 128, 64, 16, st18, scale, None), "scale")
+    expect_einval(lib.bd3_attn_bwd_dkdv(*[GOOD] * 8, 1, 1, 128, 64, 16, st18, scale, None), "scale")
+    sd = _i64([64 * 256, 64 * 256, 64] * 4)
+    expect_einval(lib.bd3_decode(GOOD, GOOD, GOOD, GOOD, 1, 1, 16, 256, 64, 16, sd, scale, GOOD, 1 << 20, None),
+                  "scale")
+    expect_einval(lib.bd3_decode_splitkv(GOOD, GOOD, GOOD, GOOD, 1, 1, 16, 256, 64, 16, 2, sd, scale, GOOD,
+                                         1 << 20, None), "scale")
 
 
 def test_tile_load_offset_stride_limit(lib):

@@ -211,3 +211,18 @@ def test_decode_scale_argument(cuda, q_len, kv_len, n_splits):
         outs.append(o)
     torch.cuda.synchronize()
     assert torch.equal(outs[0], outs[1])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("q_len,kv_len,n_splits", [(16, 700, 1), (16, 700, 3), (32, 1000, 2), (300, 1100, 1),
+                                                   (300, 1100, 3)])
+def test_decode_large_logits(cuda, record_error, q_len, kv_len, n_splits):
+    """Scores with a standard deviation near 10 on every decode path: exact
+    fp32 scores scaled in fp32, within the output bar."""
+    B, H, bs = 1, 3, 16
+    q, k, v = decode_inputs(B, H, q_len, kv_len, seed=q_len * 7 + n_splits)
+    q = bf16_round(q * 10)
+    o = splitkv_capi(*(t.to(cuda, torch.bfloat16) for t in (q, k, v)), bs, n_splits)
+    ref = decode_attention(q, k, v, bs)
+    torch.cuda.synchronize()
+    record_error("O max-abs", max_abs(o, ref), OUT_TOL)

@@ -14,7 +14,7 @@ weight (references: model/bd3lm.py:10-52, kernels/BlockSparseDecodeAttention.py:
     ones: P = 1 and dS = 1 on visible pairs, so dQ_i = scale * sum of the
     visible K rows; with K_j one-hot on f(j), dQ_i[d] * 8 is an integer
     count (exact in bf16).
-  * dK/dV kernel, fed Delta = 0 and -L * log2(e) = 0, K = 0, V_j all ones,
+  * dK/dV kernel, fed Delta = 0 and -L / scale = 0, K = 0, V_j all ones,
     Q_i one-hot on g(i), dO_i one-hot on h(i): dV_j[d] counts the rows that
     see key j with h(i) = d, dK_j[d] * 8 those with g(i) = d (the transposed
     mask, exact integers).
@@ -122,7 +122,7 @@ def test_dkdv_kernel_applies_transposed_mask_exactly(cuda, n, bs):
     mask = block_diff_mask(n, bs)
     zeros = dev(np.zeros((S, D), np.float32), H, cuda)
     ones = dev(np.ones((S, D), np.float32), H, cuda)
-    planes = torch.zeros((2, 1, H, S), device=cuda, dtype=torch.float32)  # Delta = 0, -L log2(e) = 0
+    planes = torch.zeros((2, 1, H, S), device=cuda, dtype=torch.float32)  # Delta = 0, -L / scale = 0
     lse = torch.zeros((1, H, S), device=cuda, dtype=torch.float32)
     for (gname, gmap), (hname, hmap) in ((("mod64", BUCKETS["mod64"]), ("div64", BUCKETS["div64"])),
                                          (("div64", BUCKETS["div64"]), ("mod64", BUCKETS["mod64"]))):

@@ -217,3 +217,25 @@ def test_scale_argument(cuda):
     assert torch.equal(o1, o2) and torch.equal(l1, l2)
     assert torch.equal(dk1, dk2) and torch.equal(dv1, dv2)
     assert torch.equal(dq2 * 2, dq1)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("bs", [16, 4])
+def test_large_logits(cuda, record_error, bs):
+    """Scores with a standard deviation near 10 (q scaled by 10 before the
+    bf16 rounding): the kernels form each score as an exact fp32 dot product
+    of the bf16 rows and scale it in fp32, as the reference does, so O, lse
+    and the gradients stay within the bar. (Folding scale * log2(e) into a
+    bf16-rounded operand instead puts ~0.06 into the lse at this size.)"""
+    B, H, n = 1, 2, 256
+    q, k, v, do = train_inputs(B, H, n, seed=7, count=4, q_scale=10.0)
+    qd, kd, vd, dod = to_dev((q, k, v, do), cuda)
+    o, lse = fwd_capi(qd, kd, vd, bs)
+    dq, dk, dv = bwd_capi(qd, kd, vd, o, dod, lse, bs)
+    ref_o, ref_lse = bd3_attention(q, k, v, bs)
+    _, rdq, rdk, rdv = bd3_attention_grads(q, k, v, do, bs)
+    torch.cuda.synchronize()
+    record_error("O max-abs", max_abs(o, ref_o), OUT_TOL)
+    record_error("lse max-abs", max_abs(lse, ref_lse), LSE_TOL)
+    for name, got, ref in (("dQ", dq, rdq), ("dK", dk, rdk), ("dV", dv, rdv)):
+        record_error(f"{name} rel-F", rel_frobenius(got.cpu(), ref), GRAD_TOL)
