@@ -11,9 +11,11 @@
 // wave skips tiles that are dead for its rows and masks only partial ones.
 //
 // Loads: K/V tiles go global -> LDS with global_load_lds_dwordx4 into a
-// three-stage ring of swizzled tiles (bd3_swz.h), two tiles ahead: no VGPR
-// staging and no LDS store pass; each tile ends with one counted vmcnt wait
-// and a plain s_barrier (the loads of the tile after next stay in flight).
+// ring of swizzled tiles (bd3_swz.h): no VGPR staging and no LDS store pass;
+// each tile ends with one counted vmcnt wait and a plain s_barrier. Built
+// with two stages (the next tile loads during the current one) and 4
+// workgroups per CU (4 waves per SIMD, 128 VGPRs, 32 KB of LDS each); with
+// three stages (two tiles ahead) only 3 workgroups' rings fit the LDS.
 //
 // Per wave and key tile:
 //   S^T (keys x rows) = K Q^T on v_mfma_f32_32x32x16_bf16: a lane holds one
@@ -55,10 +57,10 @@ namespace {
 constexpr float kRescale = 8.0f;
 
 #ifndef BD3_FWD_OCC
-#define BD3_FWD_OCC 3
+#define BD3_FWD_OCC 4
 #endif
 #ifndef BD3_FWD_STAGES
-#define BD3_FWD_STAGES 3
+#define BD3_FWD_STAGES 2
 #endif
 
 // One class per 64-key tile for the wave (dead / full / partial, as walk
