@@ -65,23 +65,6 @@ __device__ __forceinline__ bf16x4 to_bf16x4(float a0, float a1, float a2,
   return r;
 }
 
-// The 8 bf16 values of v times c, rounded back to bf16 (round to nearest
-// even). Used to fold the softmax scale * log2(e) into a Q or K operand once
-// per wave, so the products give base-2 exponents directly.
-__device__ __forceinline__ bf16x8 scale_bf16x8(bf16x8 v, float c) {
-  return to_bf16x8((float)v[0] * c, (float)v[1] * c, (float)v[2] * c, (float)v[3] * c,
-                   (float)v[4] * c, (float)v[5] * c, (float)v[6] * c, (float)v[7] * c);
-}
-
-// A 16-register accumulator with every entry x (the starting value of an
-// MFMA chain that should add a per-row constant).
-__device__ __forceinline__ f32x16 splat16(float x) {
-  f32x16 r;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) r[i] = x;
-  return r;
-}
-
 __device__ __forceinline__ float fast_exp2(float x) {
   return __builtin_amdgcn_exp2f(x);
 }
