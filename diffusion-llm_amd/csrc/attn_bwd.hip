@@ -33,6 +33,10 @@
 #include "bd3_swz.h"
 #include "bd3_tile.h"
 
+#ifndef BD3_DQ_STAGES
+#define BD3_DQ_STAGES 3
+#endif
+
 namespace bd3 {
 namespace {
 
@@ -280,7 +284,8 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dkdv_dma_kernel(BwdArgs a) 
 template <int OCC, bool MASK16>
 __global__ __launch_bounds__(256, OCC) void attn_bwd_dq_dma_kernel(BwdArgs a) {
   constexpr int kBM = 128;  // query rows per workgroup: 4 waves x 32
-  constexpr int kStages = 3;
+  constexpr int kStages = BD3_DQ_STAGES;
+  constexpr int kAhead = kStages - 1;  // tiles requested ahead of the one being computed
   __shared__ __attribute__((aligned(1024))) __bf16 smem[kStages][2][kSwTile];  // [stage][K|V]
 
   // threadIdx / blockIdx here, unlike the other kernels: with the id
@@ -348,9 +353,10 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dq_dma_kernel(BwdArgs a) {
     vn.next(jumping);
   };
 
-  // Tiles 0 and 1 are requested before the row loads are waited for.
-  issue(0);
-  if (n_tiles > 1) issue(1);
+  // The first kAhead tiles are requested before the row loads are waited for.
+#pragma unroll
+  for (int i = 0; i < kAhead; ++i)
+    if (i < n_tiles) issue(i);
   // Delta = rowsum(dO o O) (the reference's separate op), stored for dK/dV.
   float dsum = 0.f;
 #pragma unroll
@@ -418,8 +424,8 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dq_dma_kernel(BwdArgs a) {
   vm_wait_barrier<0>();
   int cur = 0;
   for (int it = 0; it < n_tiles; ++it) {
-    const bool pf = it + 2 < n_tiles;
-    if (pf) issue(cur == 0 ? 2 : cur - 1);
+    const bool pf = it + kAhead < n_tiles;
+    if (pf) issue(cur + kAhead < kStages ? cur + kAhead : cur + kAhead - kStages);
     const int k0 = wave_uniform(tile_of(it) * kSwRows);
     const int c0 = bounds_class(cb, k0, 32, a.n);
     const int c1 = bounds_class(cb, k0 + 32, 32, a.n);
@@ -440,10 +446,10 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dq_dma_kernel(BwdArgs a) {
             dq[db] = mfma32(sw_tr_op(ks, 32 * sb + 16 * kc, 32 * db, lane), dsop[sb][kc], dq[db]);
     }
     if (pf)
-      vm_wait_barrier<4>();
+      vm_wait_barrier<4 * (kAhead - 1)>();
     else
       vm_wait_barrier<0>();
-    cur = cur == 2 ? 0 : cur + 1;
+    cur = cur + 1 == kStages ? 0 : cur + 1;
   }
 
   uint16_t* dqp = a.dq + bo.b * a.sdq.b + bo.h * a.sdq.h + (int64_t)myq * a.sdq.s;
