@@ -46,7 +46,10 @@ namespace {
 // tiles, two tiles ahead. Every live tile runs one code path over both of its 32-row
 // blocks; a block that is not fully visible to the wave's keys is masked in
 // place (MASK16: block size a multiple of 16, two tests per lane).
-template <int OCC, bool MASK16>
+// SEQ: the two 32-row blocks of a tile one after the other (a scheduling
+// barrier between them), so one block's chains are live at a time and three
+// waves fit a SIMD; otherwise their four chains are interleaved at two waves.
+template <int OCC, bool MASK16, bool SEQ>
 __global__ __launch_bounds__(256, OCC) void attn_bwd_dkdv_dma_kernel(BwdArgs a) {
   constexpr int kBK = 128;  // keys per workgroup: 4 waves x 32
   constexpr int kStages = 3;
@@ -174,6 +177,26 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dkdv_dma_kernel(BwdArgs a) 
       }
   };
 
+  // The same for one 32-row block qb (the SEQ schedule).
+  auto block_products = [&](const __bf16* qs, const __bf16* dos, const float* scal, int qb, f32x16& s,
+                            f32x16& dp) {
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) {
+      const f32x4 dr = *reinterpret_cast<const f32x4*>(&scal[64 + 32 * qb + 8 * rg + 4 * g]);
+      const f32x4 lr = *reinterpret_cast<const f32x4*>(&scal[32 * qb + 8 * rg + 4 * g]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        dp[4 * rg + j] = dr[j];
+        s[4 * rg + j] = lr[j];
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      s = mfma32(sw_row_op(qs, 32 * qb, c, lane), kreg[c], s);
+      dp = mfma32(sw_row_op(dos, 32 * qb, c, lane), vreg[c], dp);
+    }
+  };
+
   // P^T and -dS^T operands of block qb: P = exp2(s * scale * log2(e)), -dS = P o (Delta -
   // dP). A block that is not fully visible gets P = 0 on its invisible
   // pairs: with MASK16 (block size a multiple of 16) the mask is constant on
@@ -223,23 +246,44 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dkdv_dma_kernel(BwdArgs a) 
       const __bf16* qs = &smem[cur * (kStageBytes / 2)];
       const __bf16* dos = qs + kSwTile;
       const float* scal = reinterpret_cast<const float*>(qs + 2 * kSwTile);
-      bf16x8 pop[2][2], dsop[2][2];  // [row block][16-row step]
-      f32x16 sc[2], dpc[2];
-      products(qs, dos, scal, sc, dpc);
-      softmax_ops(sc[0], dpc[0], q0, 0, c0 != kFull, pop[0], dsop[0]);
-      softmax_ops(sc[1], dpc[1], q0, 1, c1 != kFull, pop[1], dsop[1]);
-      // dV += P^T dO, dK += dS^T Q with dO / Q read transposed.
+      if constexpr (SEQ) {
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb)
+        for (int qb = 0; qb < 2; ++qb) {
+          f32x16 sc, dpc;
+          block_products(qs, dos, scal, qb, sc, dpc);
+          bf16x8 pop[2], dsop[2];  // [16-row step]
+          softmax_ops(sc, dpc, q0, qb, (qb ? c1 : c0) != kFull, pop, dsop);
+          // dV += P^T dO, dK += dS^T Q with dO / Q read transposed.
 #pragma unroll
-        for (int kc = 0; kc < 2; ++kc)
+          for (int kc = 0; kc < 2; ++kc)
 #pragma unroll
-          for (int db = 0; db < 2; ++db) {
-            const bf16x8 dot = sw_tr_op(dos, 32 * qb + 16 * kc, 32 * db, lane);
-            const bf16x8 qt = sw_tr_op(qs, 32 * qb + 16 * kc, 32 * db, lane);
-            dv[db] = mfma32(pop[qb][kc], dot, dv[db]);
-            dk[db] = mfma32(dsop[qb][kc], qt, dk[db]);
-          }
+            for (int db = 0; db < 2; ++db) {
+              const bf16x8 dot = sw_tr_op(dos, 32 * qb + 16 * kc, 32 * db, lane);
+              const bf16x8 qt = sw_tr_op(qs, 32 * qb + 16 * kc, 32 * db, lane);
+              dv[db] = mfma32(pop[kc], dot, dv[db]);
+              dk[db] = mfma32(dsop[kc], qt, dk[db]);
+            }
+          if (qb == 0) __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
+        bf16x8 pop[2][2], dsop[2][2];  // [row block][16-row step]
+        f32x16 sc[2], dpc[2];
+        products(qs, dos, scal, sc, dpc);
+        softmax_ops(sc[0], dpc[0], q0, 0, c0 != kFull, pop[0], dsop[0]);
+        softmax_ops(sc[1], dpc[1], q0, 1, c1 != kFull, pop[1], dsop[1]);
+        // dV += P^T dO, dK += dS^T Q with dO / Q read transposed.
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+          for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+            for (int db = 0; db < 2; ++db) {
+              const bf16x8 dot = sw_tr_op(dos, 32 * qb + 16 * kc, 32 * db, lane);
+              const bf16x8 qt = sw_tr_op(qs, 32 * qb + 16 * kc, 32 * db, lane);
+              dv[db] = mfma32(pop[qb][kc], dot, dv[db]);
+              dk[db] = mfma32(dsop[qb][kc], qt, dk[db]);
+            }
+      }
     }
     wait_barrier(pf);
     cur = cur == 2 ? 0 : cur + 1;
@@ -465,10 +509,20 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dq_dma_kernel(BwdArgs a) {
 #ifndef BD3_DQ_OCC
 #define BD3_DQ_OCC 3
 #endif
-#ifndef BD3_KV_OCC
-#define BD3_KV_OCC 2
-#endif
 
+
+// Key groups of up to 1024 queries' tiles (n <= 1024) run the SEQ schedule at
+// three waves per SIMD, longer ones the interleaved one at two: measured
+// (dK/dV, caches evicted) 73.4 vs 76.4 us at B=8, n=1024, bs 16; 76.5 vs 80.9
+// at bs 256; 41.9 vs 45.0 at B=32, n=256; equal at n=512 and at n=1024, bs 4;
+// but 128.3 vs 121.5 us at B=4, n=2048, bs 16 and 136.9 vs 124.7 at bs 4.
+template <bool MASK16>
+void launch_dkdv(const BwdArgs& a, dim3 grid, dim3 block, hipStream_t stream) {
+  if (a.n <= 1024)
+    hipLaunchKernelGGL((attn_bwd_dkdv_dma_kernel<3, MASK16, true>), grid, block, 0, stream, a);
+  else
+    hipLaunchKernelGGL((attn_bwd_dkdv_dma_kernel<2, MASK16, false>), grid, block, 0, stream, a);
+}
 
 }  // namespace
 
@@ -486,9 +540,9 @@ hipError_t launch_attn_bwd_dkdv(const BwdArgs& a, hipStream_t stream) {
   // 128-key tiles of 4 waves.
   const dim3 grid(a.bh * (2 * a.n / 128)), block(256);
   if (a.bs % 16 == 0)
-    hipLaunchKernelGGL((attn_bwd_dkdv_dma_kernel<BD3_KV_OCC, true>), grid, block, 0, stream, a);
+    launch_dkdv<true>(a, grid, block, stream);
   else
-    hipLaunchKernelGGL((attn_bwd_dkdv_dma_kernel<BD3_KV_OCC, false>), grid, block, 0, stream, a);
+    launch_dkdv<false>(a, grid, block, stream);
   return hipGetLastError();
 }
 
