@@ -24,6 +24,12 @@
 //   one key per lane; query tiles (Q, dO, -L / scale, Delta) come through LDS.
 //   dV += P^T dO and dK += dS^T Q take P^T / dS^T straight from registers and
 //   dO / Q transposed from LDS. dK, dV are written through LDS as 16-byte rows.
+//   Two schedules of the same arithmetic: the two 32-row blocks of a query
+//   tile one after the other at 3 waves per SIMD (n <= 1024), or their four
+//   product chains interleaved at 2 waves (longer rows).
+// Every score is the exact fp32 dot product of the bf16 rows; scale and
+// log2(e) are applied in fp32 (dQ: one FMA per element; dK/dV: the chain
+// starts from -L / scale and the result is multiplied by scale * log2(e)).
 // Both load their tiles global -> LDS with global_load_lds into three-stage
 // rings of swizzled tiles (bd3_swz.h), two tiles ahead, with one counted
 // vmcnt wait and barrier per tile.
