@@ -20,8 +20,9 @@
 // Per wave and key tile:
 //   S^T (keys x rows) = K Q^T on v_mfma_f32_32x32x16_bf16: a lane holds one
 //   query row (lane % 32) and 16 of its keys per 32x32 block, so the softmax
-//   statistics are lane-local up to one permlane32 exchange. All K operands
-//   of the tile are read from LDS in one batch.
+//   statistics are lane-local up to one permlane32 exchange. The K operands
+//   come from LDS two at a time, each pair just ahead of its two products
+//   (the other waves on the SIMD cover that latency).
 //   O^T (64 x rows) += V^T P^T, V^T read from the LDS tile by
 //   ds_read_b64_tr_b16 (requested right after the S^T products, so the reads
 //   hide behind the softmax), P^T taken from the S^T registers (key order in
