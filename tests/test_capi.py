@@ -268,12 +268,15 @@ def test_workspace_sizes(lib):
     # a cached step (q_len <= 16): down to 128 keys per split, at most 16 splits
     assert [lib.bd3_decode_auto_splits(1, 12, 16, kv) for kv in (200, 544, 3584, 8192)] == [1, 4, 16, 16]
     assert lib.bd3_decode_auto_splits(2, 12, 16, 1024) == 8
-    # q_len > 64 (the prefill kernel): split only until the longest item is
-    # no longer than the whole grid's share per slot allows
-    assert lib.bd3_decode_auto_splits(1, 12, 3088, 3088) == 3
+    # q_len > 64 (the prefill kernel): no split once the items fill half the
+    # 1024 workgroup slots, else split only until the longest item is no
+    # longer than the whole grid's share per slot allows
+    assert lib.bd3_decode_auto_splits(1, 12, 3088, 3088) == 4
     assert lib.bd3_decode_auto_splits(8, 12, 2048, 2048) == 1
-    assert lib.bd3_decode_auto_splits(32, 12, 128, 4112) == 1
-    assert lib.bd3_decode_auto_splits(4, 12, 256, 4096) == 4
+    assert lib.bd3_decode_auto_splits(8, 12, 1024, 1024) == 1  # 768 items
+    assert lib.bd3_decode_auto_splits(1, 12, 8192, 8192) == 1  # 768 items
+    assert lib.bd3_decode_auto_splits(32, 12, 128, 4112) == 2  # 384 items
+    assert lib.bd3_decode_auto_splits(4, 12, 256, 4096) == 6
     assert lib.bd3_decode_auto_splits(1, 12, 128, 3584) == 14
     assert lib.bd3_decode_workspace_bytes(32, 12, 16, 4112, 64, 0) == lib.bd3_decode_workspace_bytes(
         32, 12, 16, 4112, 64, s)
