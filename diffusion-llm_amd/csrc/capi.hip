@@ -377,6 +377,10 @@ int bd3_attn_bwd(const void* q, const void* k, const void* v, const void* o, con
   const void* ptrs[8] = {q, k, v, o, dout, dq, dk, dv};
   for (int i = 0; i < 8; ++i)
     if ((st = check_tensor(ptrs[i], strides + 3 * i, names[i]))) return st;
+  // Both stages' direct-load operands (dQ: k, v; dK/dV: q, dout) are checked
+  // before the first launch, so a refused call writes nothing.
+  for (int i : {0, 1, 2, 4})
+    if ((st = check_dma_stride(strides + 3 * i, names[i]))) return st;
   if (lse == nullptr) return fail(BD3_EINVAL, "lse is NULL");
   const size_t need = bd3_attn_bwd_workspace_bytes(batch, heads, n, head_dim);
   if (workspace == nullptr || !aligned16(workspace) || workspace_bytes < need)

@@ -45,7 +45,10 @@ extern "C" {
 #define BD3_EINVAL 1
 #define BD3_EHIP 2
 
-#define BD3_ABI_VERSION 1
+/* 2: bd3_train_tile_census writes 8 values (out[1] and out[6], out[7] are
+ * the executed pairs of each kernel) and the second workspace plane of the
+ * backward holds -L / scale. */
+#define BD3_ABI_VERSION 2
 
 /* Version of this ABI (BD3_ABI_VERSION). No reference counterpart. */
 int bd3_abi_version(void);
@@ -88,6 +91,7 @@ size_t bd3_attn_bwd_workspace_bytes(int32_t batch, int32_t heads, int32_t n,
  *          q, k, v, o, dout, dq, dk, dv.
  * Preconditions: as the forward, plus n % block_size == 0 (the reference
  * asserts it, :522) and workspace_bytes >= bd3_attn_bwd_workspace_bytes().
+ * Every precondition of both stages is checked before the first launch.
  *
  * Replaces BlockSparseFlashAttention.backward's device work
  * (kernels/BlockSparseFlashAttention.py:508-562).

@@ -38,7 +38,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.bd3_abi_version() == 1
+    assert lib.bd3_abi_version() == 2
 
 
 @pytest.mark.parametrize("n,bs", [(128, 1), (128, 16), (256, 4), (256, 100), (384, 64), (512, 512),
@@ -175,6 +175,18 @@ def test_bwd_validation(lib):
     expect_einval(lib.bd3_attn_bwd_dkdv(*[GOOD] * 8, 1, 1, 128, 64, 5, st18, 0.125, None), "block_size")
     expect_einval(lib.bd3_attn_bwd_dkdv(GOOD, GOOD, GOOD, GOOD + 8, *[GOOD] * 4, 1, 1, 128, 64, 16, st18,
                                         0.125, None), "dout")
+
+
+def test_bwd_refuses_before_any_launch(lib):
+    """bd3_attn_bwd checks the direct-load stride limit of both stages' tile
+    operands (dQ: k, v; dK/dV: q, dout) before its first launch, so a refused
+    call has written nothing (fake device pointers, no GPU needed)."""
+    need = lib.bd3_attn_bwd_workspace_bytes(1, 1, 128, 64)
+    for slot, name in ((0, "q"), (1, "k"), (2, "v"), (4, "dout")):
+        st = [64 * 256, 64 * 256, 64] * 8
+        st[3 * slot + 2] = 1 << 24
+        expect_einval(lib.bd3_attn_bwd(*[GOOD] * 9, GOOD, need, 1, 1, 128, 64, 16, _i64(st), 0.125, None),
+                      f"{name} sequence stride")
 
 
 @pytest.mark.parametrize("scale", [0.0, -0.125, float("nan"), float("inf")])
