@@ -820,8 +820,24 @@ def main(argv=None) -> int:
             f"({result['cpu_baseline']['sample']})")
     else:
         result["cpu_baseline"] = None
+    log_sections(result)
     print(json.dumps(result), flush=True)
     return 0
+
+
+def log_sections(result: dict) -> None:
+    """One JSONL record per bench section in RESULTS_DIR (perf.harness.log_result,
+    the reference's bench/harness.py:75-91 record: config, timing, environment
+    and the section's figures)."""
+    from perf.harness import RESULTS_DIR, log_result
+    train = {k: v for k, v in result.items()
+             if k not in ("config", "decode", "decode_batch1", "kv_cache", "sampling", "dit_glue", "e2e", "sweep",
+                          "long_sequences")}
+    log_result("attention_train", result["config"], timing=result.get("step_ms"), **train)
+    for key in ("decode", "decode_batch1", "kv_cache", "sampling", "dit_glue", "e2e", "sweep", "long_sequences"):
+        if key in result:
+            log_result(key, {"workload": key}, figures=result[key])
+    log(f"results appended to {RESULTS_DIR}/*.jsonl")
 
 
 if __name__ == "__main__":

@@ -18,13 +18,23 @@ with the timed call for HBM.
 
     samples = time_calls(fn, reps=30, warmup=5)   # flush, event, fn(), event
     samples.median_ms, samples.quantile_ms(0.2), samples.mean_ms
+
+Results are kept as the reference keeps them (bench/harness.py:62-91):
+`check(out, ref)` compares in float64 (pass iff |out - ref| <= atol + rtol *
+|ref| everywhere) and `log_result(name, config, timing, check, **metrics)`
+appends one JSON record per run to RESULTS_DIR/<name>.jsonl.
 """
 from __future__ import annotations
 
 import ctypes
+import json
+import os
 import statistics
 import time
 from collections.abc import Callable, Sequence
+from dataclasses import asdict, dataclass
+from datetime import datetime, timezone
+from pathlib import Path
 from typing import Any
 
 import torch
@@ -210,3 +220,81 @@ def shader_clock_ghz(lib: ctypes.CDLL, device: torch.device, workgroups: int = 1
     return {"median": med, "min": ghz[0], "max": ghz[-1], "wall_rate_khz": rate.value,
             "bf16_peak_tflops": 256 * 4096 * med * 1e9 / 1e12,
             "probe": f"{workgroups} workgroups x 4 waves, {iters} rounds of 4 independent 32x32x16 bf16 MFMAs"}
+
+
+RESULTS_DIR = Path(os.environ.get("RESULTS_DIR", "results"))
+
+
+@dataclass
+class Check:
+    """Outcome of `check`: pass / fail plus the float64 error figures."""
+    passed: bool
+    max_abs: float
+    max_rel: float
+    cosine: float
+
+
+def check(out: torch.Tensor, ref: torch.Tensor, atol: float = 1e-5, rtol: float = 1e-4) -> Check:
+    """Element-wise comparison in float64: passes iff every |out - ref| <=
+    atol + rtol * |ref| (a NaN anywhere fails). max_rel divides by |ref|
+    clamped at 1e-12 and is informational (it grows where ref ~ 0)."""
+    o = out.detach().to("cpu", torch.float64).reshape(-1)
+    r = ref.detach().to("cpu", torch.float64).reshape(-1)
+    if o.shape != r.shape:
+        raise ValueError(f"shape mismatch: {tuple(out.shape)} vs {tuple(ref.shape)}")
+    diff = (o - r).abs()
+    ok = bool(torch.all(diff <= atol + rtol * r.abs()))  # NaN compares false
+    den = float(o.norm() * r.norm())
+    return Check(passed=ok,
+                 max_abs=float(diff.max()) if diff.numel() else 0.0,
+                 max_rel=float((diff / r.abs().clamp_min(1e-12)).max()) if diff.numel() else 0.0,
+                 cosine=float(torch.dot(o, r)) / den if den > 0 else float("nan"))
+
+
+def _timing_record(timing: Any) -> dict | None:
+    if timing is None:
+        return None
+    if isinstance(timing, Samples):
+        return {"median_ms": timing.median_ms, "p20_ms": timing.p20_ms, "p80_ms": timing.p80_ms,
+                "mean_ms": timing.mean_ms, "n_iters": timing.n_iters}
+    if isinstance(timing, dict):
+        return timing
+    return asdict(timing)
+
+
+def _environment() -> dict:
+    env = {"torch": torch.__version__, "hip": getattr(torch.version, "hip", None)}
+    if torch.cuda.is_available():
+        env["gpu"] = torch.cuda.get_device_name()
+        props = torch.cuda.get_device_properties(torch.cuda.current_device())
+        env["gcn_arch"] = getattr(props, "gcnArchName", None)
+        env["compute_units"] = props.multi_processor_count
+    else:
+        env["gpu"] = "cpu"
+    try:
+        from kernels._native import LIB_PATH, lib
+        if LIB_PATH.exists():
+            env["bd3_abi_version"] = lib().bd3_abi_version()
+    except Exception:  # the record is still useful without the library
+        pass
+    return env
+
+
+def log_result(name: str, config: dict, timing: Any = None, check: Check | None = None, **metrics: Any) -> Path:
+    """Append one run to RESULTS_DIR/<name>.jsonl: UTC time, the config, the
+    timing (a Samples, a dict or a dataclass), the check, the environment
+    (GPU, torch / HIP versions, library ABI) and any extra metrics. Returns
+    the file written."""
+    record = {
+        "time": datetime.now(timezone.utc).isoformat(timespec="seconds"),
+        "config": config,
+        "timing": _timing_record(timing),
+        "check": asdict(check) if check is not None else None,
+        "env": _environment(),
+        **metrics,
+    }
+    RESULTS_DIR.mkdir(parents=True, exist_ok=True)
+    path = RESULTS_DIR / f"{name}.jsonl"
+    with path.open("a") as f:
+        f.write(json.dumps(record, default=str) + "\n")
+    return path

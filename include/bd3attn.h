@@ -115,7 +115,10 @@ int bd3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
  * 2n=8192); larger calls return BD3_EINVAL. Every call on one GPU shares
  * that GPU's array: calls that overlap on one GPU (different streams or
  * threads, no ordering between them) race and must not be made. The calling
- * thread's current device must be the device of `stream`.
+ * thread's current device must be the device of `stream`. Under HIP graph
+ * capture: make one eager call on the device first (it looks up the array's
+ * device address); later calls only enqueue the kernels and can be captured
+ * and replayed (the planes are fully rewritten by every call).
  */
 #define BD3_NOALLOC_MAX_ROWS (1 << 20)
 int bd3_attn_bwd_noalloc(const void* q, const void* k, const void* v,
