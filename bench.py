@@ -4,9 +4,10 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 
 Headline: one step = BD3-LM training attention
-forward + backward (bd3_attn_fwd, bd3_attn_bwd_dq, bd3_attn_bwd_dkdv through
-the C ABI, launched one after the other on one stream; --graph replays them
-from one captured HIP graph instead) at
+forward + backward (bd3_attn_fwd, then the backward's Delta pass
+bd3_attn_bwd_delta and its main launch bd3_attn_bwd_main, through the C ABI,
+launched one after the other on one stream; --graph replays them from
+captured HIP graphs instead) at
 B=8, L=1024 (sequence 2048), H=12, d=64, block 16, bf16, q/k/v/dO ~ N(0,1)
 from seed 0, resident in HBM. value = useful fwd+bwd FLOPs per second:
 3.5 x 4*d*B*H*(n^2 + n*bs) (the reference's convention,
@@ -104,11 +105,11 @@ class TrainStep:
         self.o = torch.empty_like(self.q)
         self.lse = torch.empty((B, H, 2 * n), device=device, dtype=torch.float32)
         self.dq, self.dk, self.dv = (torch.empty_like(self.q) for _ in range(3))
-        self.delta = torch.empty((2, B, H, 2 * n), device=device, dtype=torch.float32)  # Delta, L * log2(e)
+        self.delta = torch.empty((2, B, H, 2 * n), device=device, dtype=torch.float32)  # Delta, -L / scale
         self.lib = lib()
         self.fwd_strides = strides(self.q, self.k, self.v, self.o)
-        self.dq_strides = strides(self.q, self.k, self.v, self.o, self.do, self.dq)
-        self.dkdv_strides = strides(self.q, self.k, self.v, self.do, self.dk, self.dv)
+        self.delta_strides = strides(self.o, self.do)
+        self.main_strides = strides(self.q, self.k, self.v, self.do, self.dq, self.dk, self.dv)
         self.stream = stream_of(self.q)
         self.p = {name: ptr(getattr(self, name)) for name in
                   ("q", "k", "v", "o", "lse", "do", "dq", "dk", "dv", "delta")}
@@ -120,25 +121,25 @@ class TrainStep:
         check(self.lib.bd3_attn_fwd(p["q"], p["k"], p["v"], p["o"], p["lse"], self.B, self.H, self.n, D,
                                     self.bs, self.fwd_strides, self.scale, self.stream))
 
-    def bwd_dq(self):
-        """bd3_attn_bwd_dq: dQ and Delta (first half of bd3_attn_bwd)."""
+    def bwd_delta(self):
+        """bd3_attn_bwd_delta: Delta and -L / scale (the backward's first launch)."""
         from kernels._native import check
         p = self.p
-        check(self.lib.bd3_attn_bwd_dq(p["q"], p["k"], p["v"], p["o"], p["do"], p["lse"], p["dq"],
-                                       p["delta"], self.B, self.H, self.n, D, self.bs, self.dq_strides,
-                                       self.scale, self.stream))
+        check(self.lib.bd3_attn_bwd_delta(p["o"], p["do"], p["lse"], p["delta"], self.B, self.H, self.n, D, self.bs,
+                                          self.delta_strides, self.scale, self.stream))
 
-    def bwd_dkdv(self):
-        """bd3_attn_bwd_dkdv: dK, dV (second half of bd3_attn_bwd)."""
+    def bwd_main(self):
+        """bd3_attn_bwd_main: every dQ and dK/dV item in one launch."""
         from kernels._native import check
         p = self.p
-        check(self.lib.bd3_attn_bwd_dkdv(p["q"], p["k"], p["v"], p["do"], p["lse"], p["delta"], p["dk"],
-                                         p["dv"], self.B, self.H, self.n, D, self.bs, self.dkdv_strides,
-                                         self.scale, self.stream))
+        check(self.lib.bd3_attn_bwd_main(p["q"], p["k"], p["v"], p["do"], p["lse"], p["delta"], p["dq"], p["dk"],
+                                         p["dv"], self.B, self.H, self.n, D, self.bs, self.main_strides, self.scale,
+                                         self.stream))
 
     def bwd(self):
-        self.bwd_dq()
-        self.bwd_dkdv()
+        """bd3_attn_bwd's two launches."""
+        self.bwd_delta()
+        self.bwd_main()
 
     def useful_flops(self):
         return 3.5 * useful_fwd_flops(self.B, self.H, self.n, self.bs)
@@ -219,9 +220,9 @@ def time_train(step: TrainStep, steps: int, warmup: int, use_graph: bool = False
         flush_caches()
         ev[2].record(stream)
         if graphs is None:
-            step.bwd_dq()
+            step.bwd_delta()
             ev[3].record(stream)
-            step.bwd_dkdv()
+            step.bwd_main()
         else:
             bwd_fn()
             ev[3].record(stream)
@@ -231,7 +232,7 @@ def time_train(step: TrainStep, steps: int, warmup: int, use_graph: bool = False
     total = Samples([e[0].elapsed_time(e[1]) + e[2].elapsed_time(e[4]) for e in events])
     spans = {"fwd": (0, 1), "bwd": (2, 4)}
     if graphs is None:
-        spans.update(bwd_dq=(2, 3), bwd_dkdv=(3, 4))
+        spans.update(bwd_delta=(2, 3), bwd_main=(3, 4))
     per = {k: Samples([e[a].elapsed_time(e[b]) for e in events]) for k, (a, b) in spans.items()}
     kernel_ms = {k: v.median_ms for k, v in per.items()}
     kernel_mean_ms = {k: v.mean_ms for k, v in per.items()}
@@ -605,9 +606,10 @@ def census(n, bs):
     from kernels._native import lib
     out = (ctypes.c_int64 * 8)()
     lib().bd3_train_tile_census(n, bs, out)
-    return {"useful_pairs": out[0], "executed_pairs": {"fwd": out[1], "bwd_dq": out[6], "bwd_dkdv": out[7]},
-            "useful_fraction_of_executed": {"fwd": out[0] / out[1], "bwd_dq": out[0] / out[6],
-                                            "bwd_dkdv": out[0] / out[7]}}
+    return {"useful_pairs": out[0], "executed_pairs": {"fwd": out[1], "bwd_dq_items": out[6],
+                                                        "bwd_dkdv_items": out[7]},
+            "useful_fraction_of_executed": {"fwd": out[0] / out[1], "bwd_dq_items": out[0] / out[6],
+                                            "bwd_dkdv_items": out[0] / out[7]}}
 
 
 def train_record(step: "TrainStep", t: dict) -> dict:
@@ -619,8 +621,9 @@ def train_record(step: "TrainStep", t: dict) -> dict:
     own figures, dense FLOPs 4*B*H*L^2*d with L = 2n, fwd_tflops =
     fwd_flops / fwd time, bwd_tflops = 2.5 fwd_flops / bwd time
     (bench/attention_bench.py:89,98-99). kernel_formed_tflops: the products
-    each kernel forms (forward S, PV; dQ kernel S, dP, dQ; dK/dV kernel S, dP,
-    dV, dK: recomputation included) per second."""
+    each kernel forms (forward S, PV; the backward's main launch S, dP, dQ for
+    its dQ items and S, dP, dV, dK for its dK/dV items: recomputation
+    included) per second."""
     B, H, n, bs = step.B, step.H, step.n, step.bs
     fwd = useful_fwd_flops(B, H, n, bs)
     ms = t["step_ms"]["median"]
@@ -638,7 +641,7 @@ def train_record(step: "TrainStep", t: dict) -> dict:
         rec["reference_convention"] = {"fwd_ms": km["fwd"], "bwd_ms": bwd_ms, "dense_fwd_flops": dense,
                                        "fwd_tflops": dense / (km["fwd"] * 1e-3) / 1e12,
                                        "bwd_tflops": 2.5 * dense / (bwd_ms * 1e-3) / 1e12}
-        formed = {"fwd": 1.0, "bwd_dq": 1.5, "bwd_dkdv": 2.0}
+        formed = {"fwd": 1.0, "bwd_main": 3.5}
         rec["kernel_formed_tflops"] = {k: formed[k] * fwd / (km[k] * 1e-3) / 1e12 for k in formed if k in km}
     return rec
 
@@ -710,19 +713,19 @@ def main(argv=None) -> int:
     log(f"config1 fwd+bwd ({t['launch']}, caches evicted before fwd and before bwd): {ms * 1e3:.1f} us/step median "
         f"(p20 {t['step_ms']['p20'] * 1e3:.1f}, p80 {t['step_ms']['p80'] * 1e3:.1f}; back to back warm "
         f"{t['warm_ms_per_step'] * 1e3:.1f}) -> {tflops:.1f} useful TFLOP/s")
-    if "bwd_dq" in per:
-        log(f"  fwd {per['fwd'] * 1e3:.1f} us, dQ {per['bwd_dq'] * 1e3:.1f} us, dK/dV {per['bwd_dkdv'] * 1e3:.1f} us")
+    if "bwd_main" in per:
+        log(f"  fwd {per['fwd'] * 1e3:.1f} us, bwd Delta pass {per['bwd_delta'] * 1e3:.1f} us, "
+            f"bwd main launch {per['bwd_main'] * 1e3:.1f} us")
 
     # Dominant kernel's roofline: its algorithmic (useful) FLOPs per launch,
     # the FA2 credit of the products it owns (forward 1x the useful forward
-    # FLOPs; dQ kernel 0.5x: the dQ product; dK/dV kernel 2x: S, dP, dV, dK),
+    # FLOPs; the backward's main launch 2.5x: all of the backward's products),
     # over its average (mean) launch duration inside the timed steps.
     fwd_flops = useful_fwd_flops(B, H, n, bs)
-    credit = {"fwd": 1.0, "bwd_dq": 0.5, "bwd_dkdv": 2.0}
-    names = {"fwd": "attn_fwd_dma_kernel", "bwd_dq": "attn_bwd_dq_dma_kernel",
-             "bwd_dkdv": "attn_bwd_dkdv_dma_kernel"}
+    credit = {"fwd": 1.0, "bwd_main": 2.5}
+    names = {"fwd": "attn_fwd_dma_kernel", "bwd_main": "attn_bwd_kernel"}
     per = {k: v for k, v in per.items() if k in credit}
-    dom = max(per, key=per.get) if per else "bwd_dkdv"
+    dom = max(per, key=per.get) if per else "bwd_main"
     dom_flops = credit[dom] * fwd_flops
     dom_mean = t["kernel_mean_ms"].get(dom)
     achieved = dom_flops / (dom_mean * 1e-3) / 1e12 if dom_mean else None
@@ -750,7 +753,7 @@ def main(argv=None) -> int:
                      "kernel": names[dom], "algorithmic_flops_per_launch": dom_flops,
                      "mean_launch_us": dom_mean * 1e3 if dom_mean else None,
                      "credit": f"{credit[dom]} x useful forward FLOPs (FA2 convention: backward = 2.5x forward, "
-                               "dQ kernel owns the dQ product, dK/dV kernel S, dP, dV, dK)"},
+                               "all of it owned by the backward's main launch; the Delta pass owns none)"},
     }
     del step
     torch.cuda.empty_cache()

@@ -55,15 +55,62 @@ namespace {
 // SEQ: the two 32-row blocks of a tile one after the other (a scheduling
 // barrier between them), so one block's chains are live at a time and three
 // waves fit a SIMD; otherwise their four chains are interleaved at two waves.
-template <int OCC, bool MASK16, bool SEQ>
-__global__ __launch_bounds__(256, OCC) void attn_bwd_dkdv_dma_kernel(BwdArgs a) {
+// Stage layout of the dK/dV ring (bytes): Q tile [0, 8K), dO tile [8K, 16K),
+// row scalars [16K, 17K): -L / scale of the 64 rows, then Delta, then both
+// again (the load that fetches them writes 1 KB).
+constexpr int kDkdvStages = 3;
+constexpr int kDkdvStageBytes = 4 * kSwTile + 1024;
+constexpr int kDkdvLdsBytes = kDkdvStages * kDkdvStageBytes;
+constexpr int kDqStages = BD3_DQ_STAGES;
+constexpr int kDqLdsBytes = kDqStages * 2 * kSwTile * 2;  // [stage][K | V] tiles
+constexpr int kBwdLdsBytes = kDkdvLdsBytes > kDqLdsBytes ? kDkdvLdsBytes : kDqLdsBytes;
+
+// dK/dV epilogue (every wave is past its last barrier, no load in flight):
+// each wave transposes its 32 keys x 64 d of dK, then dV, through its own
+// padded LDS slice into row-major bf16, then writes 16-byte row chunks.
+__device__ __forceinline__ void dkdv_store(const BwdArgs& a, __bf16* smem, int b, int h, int kw, int wave, int lane,
+                                           const f32x16 (&dk)[2], const f32x16 (&dv)[2]) {
+  const int l32 = lane & 31;
+  const int g = lane >> 5;
+  __bf16* tile = &smem[0] + wave * kTileElems;
+  uint16_t* outs[2] = {a.dk + b * a.sdk.b + h * a.sdk.h, a.dv + b * a.sdv.b + h * a.sdv.h};
+  const int64_t ostr[2] = {a.sdk.s, a.sdv.s};
+#pragma unroll
+  for (int which = 0; which < 2; ++which) {
+    const float mul = which == 0 ? -a.scale : 1.f;  // dK was accumulated from -dS
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int krow = 8 * (r >> 2) + 4 * g + (r & 3);
+        const float x = (which == 0 ? dk[db][r] : dv[db][r]) * mul;
+        tile[krow * kLdsStride + 32 * db + l32] = (__bf16)x;
+      }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = (lane >> 3) + 8 * j;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(&tile[row * kLdsStride + 8 * (lane & 7)]);
+      st16(outs[which] + (int64_t)(kw + row) * ostr[which] + 8 * (lane & 7), v);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+// One dK/dV item: key tile `rank` (clean key tiles 0 .. n/128 - 1 first, the
+// heaviest: clean keys are seen by the most rows; then the noisy ones) of
+// (batch*head) bh, with the ring in `smem` (kDkdvLdsBytes).
+// DIAG: a noisy key tile with a block size dividing 32, whose two query tiles
+// are its own 128 rows: wave w's keys are seen only by the rows of 32-row
+// block w % 2 of tile w / 2, so each wave computes that one block (exactly
+// what the tile loop accumulates; its other blocks contribute zeros).
+template <bool MASK16, bool SEQ, bool DIAG>
+__device__ __forceinline__ void dkdv_item(const BwdArgs& a, __bf16* smem, int bh, int rank) {
   constexpr int kBK = 128;  // keys per workgroup: 4 waves x 32
-  constexpr int kStages = 3;
-  // Stage layout (bytes): Q tile [0, 8K), dO tile [8K, 16K), row scalars
-  // [16K, 17K): -L / scale of the 64 rows, then Delta, then both again (the
-  // load that fetches them writes 1 KB).
-  constexpr int kStageBytes = 4 * kSwTile + 1024;
-  __shared__ __attribute__((aligned(1024))) __bf16 smem[kStages * kStageBytes / 2];
+  constexpr int kStages = kDkdvStages;
+  constexpr int kStageBytes = kDkdvStageBytes;
 
   const int tid = wi_x();
   const int lane = tid & 63;
@@ -71,10 +118,11 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dkdv_dma_kernel(BwdArgs a) 
   const int l32 = lane & 31;
   const int g = lane >> 5;
 
-  // Heaviest key tiles first: clean tiles are seen by the most rows.
-  const BlockOrder bo(a.bh, a.heads);
   const int tiles_half = a.n / kBK;
-  const int k0 = bo.rank < tiles_half ? a.n + bo.rank * kBK : (bo.rank - tiles_half) * kBK;
+  const int k0 = rank < tiles_half ? a.n + rank * kBK : (rank - tiles_half) * kBK;
+  struct {
+    int bh, b, h;
+  } bo = {bh, bh / a.heads, bh - (bh / a.heads) * a.heads};
 
   const uint16_t* qp = uniform_ptr(a.q + bo.b * a.sq.b + bo.h * a.sq.h);
   const uint16_t* dop = uniform_ptr(a.dout + bo.b * a.sdo.b + bo.h * a.sdo.h);
@@ -96,7 +144,6 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dkdv_dma_kernel(BwdArgs a) 
   const int n_first = wave_uniform(qr.t1 - qr.t0);
   const int n_tiles = n_first + wave_uniform(qr.t3 - qr.t2);
   auto tile_of = [&](int i) { return i < n_first ? t0 + i : t2 + (i - n_first); };
-
   // Wave w fills 1 KB blocks 2w, 2w+1 (rows 16w .. 16w+15) of the Q and dO
   // tiles; wave 0 also fetches the row scalars: lane L reads 16 bytes of L
   // (L % 32 < 16) or Delta, rows 4 (L % 16) .. +3.
@@ -239,6 +286,33 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dkdv_dma_kernel(BwdArgs a) 
 
   // Every key group is seen by its own block, so n_tiles >= 1.
   vm_wait_barrier<0>();
+  if constexpr (DIAG) {
+    // Both query tiles are in stages 0 and 1 (no further loads); the
+    // barrier after the block keeps the epilogue's LDS reuse behind every
+    // wave's reads, as the tile loop's last barrier does.
+    const int st = wave >> 1, qb = wave & 1;
+    const int q0 = wave_uniform((t0 + st) * kSwRows);
+    const int cls = bounds_class(cb, q0 + 32 * qb, 32, a.n);
+    if (cls != kNone) {
+      const __bf16* qs = &smem[st * (kStageBytes / 2)];
+      const __bf16* dos = qs + kSwTile;
+      const float* scal = reinterpret_cast<const float*>(qs + 2 * kSwTile);
+      f32x16 sc, dpc;
+      block_products(qs, dos, scal, qb, sc, dpc);
+      bf16x8 pop[2], dsop[2];  // [16-row step]
+      softmax_ops(sc, dpc, q0, qb, cls != kFull, pop, dsop);
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+        for (int db = 0; db < 2; ++db) {
+          dv[db] = mfma32(pop[kc], sw_tr_op(dos, 32 * qb + 16 * kc, 32 * db, lane), dv[db]);
+          dk[db] = mfma32(dsop[kc], sw_tr_op(qs, 32 * qb + 16 * kc, 32 * db, lane), dk[db]);
+        }
+    }
+    vm_wait_barrier<0>();
+    dkdv_store(a, smem, bo.b, bo.h, kw, wave, lane, dk, dv);
+    return;
+  }
   int cur = 0;
   for (int it = 0; it < n_tiles; ++it) {
     const bool pf = it + 2 < n_tiles;
@@ -295,34 +369,7 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dkdv_dma_kernel(BwdArgs a) 
     cur = cur == 2 ? 0 : cur + 1;
   }
 
-  // Epilogue (every wave is past the last barrier, no load in flight): each
-  // wave transposes its 32 keys x 64 d of dK, then dV, through its own padded
-  // LDS slice into row-major bf16, then writes 16-byte row chunks.
-  __bf16* tile = &smem[0] + wave * kTileElems;
-  uint16_t* outs[2] = {a.dk + bo.b * a.sdk.b + bo.h * a.sdk.h, a.dv + bo.b * a.sdv.b + bo.h * a.sdv.h};
-  const int64_t ostr[2] = {a.sdk.s, a.sdv.s};
-#pragma unroll
-  for (int which = 0; which < 2; ++which) {
-    const float mul = which == 0 ? -a.scale : 1.f;  // dK was accumulated from -dS
-#pragma unroll
-    for (int db = 0; db < 2; ++db)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int krow = 8 * (r >> 2) + 4 * g + (r & 3);
-        const float x = (which == 0 ? dk[db][r] : dv[db][r]) * mul;
-        tile[krow * kLdsStride + 32 * db + l32] = (__bf16)x;
-      }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int row = (lane >> 3) + 8 * j;
-      const u32x4 v = *reinterpret_cast<const u32x4*>(&tile[row * kLdsStride + 8 * (lane & 7)]);
-      st16(outs[which] + (int64_t)(kw + row) * ostr[which] + 8 * (lane & 7), v);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-  }
+  dkdv_store(a, smem, bo.b, bo.h, kw, wave, lane, dk, dv);
 }
 
 // ---------------------------------------------------------------------------
@@ -331,45 +378,51 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dkdv_dma_kernel(BwdArgs a) 
 // Every live tile runs one code path over both of its 32-key blocks; a block
 // that is not fully visible to the wave's rows is masked in place (MASK16:
 // block size a multiple of 16, two tests per lane).
-template <int OCC, bool MASK16>
-__global__ __launch_bounds__(256, OCC) void attn_bwd_dq_dma_kernel(BwdArgs a) {
+// One dQ item: 128-row query tile `rank` (heaviest first: rank r is tile
+// n/128 - 1 - r/2 of the clean half for even r, of the noisy half for odd r)
+// of (batch*head) bh, with the ring in `smem` (kDqLdsBytes). Delta and the
+// rows' L come from the Delta pass.
+template <bool MASK16>
+__device__ __forceinline__ void dq_item(const BwdArgs& a, __bf16* smem, int bh, int rank) {
   constexpr int kBM = 128;  // query rows per workgroup: 4 waves x 32
-  constexpr int kStages = BD3_DQ_STAGES;
+  constexpr int kStages = kDqStages;
   constexpr int kAhead = kStages - 1;  // tiles requested ahead of the one being computed
-  __shared__ __attribute__((aligned(1024))) __bf16 smem[kStages][2][kSwTile];  // [stage][K|V]
+  auto stage_k = [&](int st) { return smem + st * (2 * kSwTile); };
+  auto stage_v = [&](int st) { return smem + st * (2 * kSwTile) + kSwTile; };
 
-  // threadIdx / blockIdx here, unlike the other kernels: with the id
-  // builtins the allocator spills one more VGPR in this kernel's tile loop
-  // (2 us slower at configs[1], outputs identical).
+  // threadIdx here, unlike the other kernels: with the id builtin the
+  // allocator spills one more VGPR in this tile loop (2 us slower at
+  // configs[1], outputs identical).
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = wave_uniform(tid >> 6);
   const int l32 = lane & 31;
   const int g = lane >> 5;
 
-  const BlockOrder bo((int)blockIdx.x, a.bh, a.heads);
+  struct {
+    int bh, b, h;
+  } bo = {bh, bh / a.heads, bh - (bh / a.heads) * a.heads};
   const int tiles_half = a.n / kBM;
-  const int t = tiles_half - 1 - (bo.rank >> 1);
-  const int q0 = ((bo.rank & 1) ? 0 : a.n) + t * kBM;
+  const int t = tiles_half - 1 - (rank >> 1);
+  const int q0 = ((rank & 1) ? 0 : a.n) + t * kBM;
 
   const uint16_t* qp = a.q + bo.b * a.sq.b + bo.h * a.sq.h;
   const uint16_t* kp = uniform_ptr(a.k + bo.b * a.sk.b + bo.h * a.sk.h);
   const uint16_t* vp = uniform_ptr(a.v + bo.b * a.sv.b + bo.h * a.sv.h);
-  const uint16_t* opp = a.o + bo.b * a.so.b + bo.h * a.so.h;
   const uint16_t* dop = a.dout + bo.b * a.sdo.b + bo.h * a.sdo.h;
   const int64_t rowbase = (int64_t)bo.bh * 2 * a.n;
 
   const int qrow0 = q0 + 32 * wave;
   const int myq = qrow0 + l32;
-  bf16x8 qreg[4], doreg[4], oreg[4];
+  bf16x8 qreg[4], doreg[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     const int col = 16 * c + 8 * g;
     qreg[c] = __builtin_bit_cast(bf16x8, ld16(qp + (int64_t)myq * a.sq.s + col));
     doreg[c] = __builtin_bit_cast(bf16x8, ld16(dop + (int64_t)myq * a.sdo.s + col));
-    oreg[c] = __builtin_bit_cast(bf16x8, ld16(opp + (int64_t)myq * a.so.s + col));
   }
   const float lse_row = a.lse[rowbase + myq];
+  const float drow = a.delta[rowbase + myq];
 
   const KeyRanges kr = train_key_ranges(q0, kBM, a.n, a.bs, kSwRows);
   const int t0 = wave_uniform(kr.t0), t2 = wave_uniform(kr.t2);
@@ -387,7 +440,7 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dq_dma_kernel(BwdArgs a) {
     voff[j] = (uint32_t)(2 * (r * (int)a.sv.s + ch));
   }
   const int64_t kstep = (int64_t)kSwRows * a.sk.s, vstep = (int64_t)kSwRows * a.sv.s;
-  const uint32_t lds_w = lds_addr(&smem[0][0][0]) + (uint32_t)wave * 2048u;
+  const uint32_t lds_w = lds_addr(smem) + (uint32_t)wave * 2048u;
   // Sources of the next tile to request, walked tile by tile.
   TileWalk walk(t0, n_first, t2);
   TilePtr kn(kp, 2 * kstep, t0, n_first, t2), vn(vp, 2 * vstep, t0, n_first, t2);
@@ -407,19 +460,7 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dq_dma_kernel(BwdArgs a) {
 #pragma unroll
   for (int i = 0; i < kAhead; ++i)
     if (i < n_tiles) issue(i);
-  // Delta = rowsum(dO o O) (the reference's separate op), stored for dK/dV.
-  float dsum = 0.f;
-#pragma unroll
-  for (int c = 0; c < 4; ++c)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) dsum = fmaf((float)doreg[c][j], (float)oreg[c][j], dsum);
-  const float drow = sum_xor32(dsum);
   const float lrow = lse_row * kLog2e;
-  const float lseed = -lse_row / a.scale;
-  if (g == 0) {
-    a.delta[rowbase + myq] = drow;
-    a.delta[(int64_t)a.bh * 2 * a.n + rowbase + myq] = lseed;  // second plane: -L / scale for dK/dV
-  }
 #pragma unroll
   for (int c = 0; c < 4; ++c) asm volatile("" ::"v"(qreg[c]), "v"(doreg[c]));
   const RowIntervals riv = train_row_intervals(myq, a.n, a.bs);
@@ -481,8 +522,8 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dq_dma_kernel(BwdArgs a) {
     const int c1 = bounds_class(cb, k0 + 32, 32, a.n);
     // One code path for every live tile (the accumulators keep their registers).
     if ((c0 | c1) != kNone) {
-      const __bf16* ks = smem[cur][0];
-      const __bf16* vs = smem[cur][1];
+      const __bf16* ks = stage_k(cur);
+      const __bf16* vs = stage_v(cur);
       bf16x8 dsop[2][2];  // [key block][16-key step]
       block_ops(ks, vs, k0, 0, c0 != kFull, dsop[0]);
       block_ops(ks, vs, k0, 1, c1 != kFull, dsop[1]);
@@ -512,43 +553,88 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_dq_dma_kernel(BwdArgs a) {
                     dq[db][4 * rg + 3] * a.scale);
 }
 
-#ifndef BD3_DQ_OCC
-#define BD3_DQ_OCC 3
-#endif
+// Delta = rowsum(dO o O) (the reference's separate torch op,
+// kernels/BlockSparseFlashAttention.py:525) and -L / scale (the dK/dV score
+// chains' seed) of every row, into the two workspace planes: 8 lanes per row
+// (16 bytes each), 32 rows per pass of a 256-thread workgroup, kPasses
+// passes with every load issued before the first use. Bound by reading O
+// and dO once.
+__global__ __launch_bounds__(256) void attn_bwd_delta_kernel(BwdArgs a) {
+  constexpr int kPasses = 4;
+  const int tid = wi_x();
+  const int grp = tid >> 3, part = tid & 7;
+  const int rows_bh = 2 * a.n;
+  u32x4 ov[kPasses], dv[kPasses];
+  int64_t row[kPasses];
+#pragma unroll
+  for (int p = 0; p < kPasses; ++p) {
+    const int64_t r = (int64_t)wg_x() * (32 * kPasses) + 32 * p + grp;
+    const int bh = (int)(r / rows_bh), s = (int)(r - (int64_t)bh * rows_bh);
+    const int b = bh / a.heads, h = bh - b * a.heads;
+    row[p] = r;
+    ov[p] = ld16(a.o + b * a.so.b + h * a.so.h + (int64_t)s * a.so.s + 8 * part);
+    dv[p] = ld16(a.dout + b * a.sdo.b + h * a.sdo.h + (int64_t)s * a.sdo.s + 8 * part);
+  }
+  float lse[kPasses];
+#pragma unroll
+  for (int p = 0; p < kPasses; ++p) lse[p] = part == 0 ? a.lse[row[p]] : 0.f;
+#pragma unroll
+  for (int p = 0; p < kPasses; ++p) {
+    const bf16x8 o8 = __builtin_bit_cast(bf16x8, ov[p]), d8 = __builtin_bit_cast(bf16x8, dv[p]);
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sum = fmaf((float)d8[j], (float)o8[j], sum);
+    sum += shfl_xor(sum, 1);
+    sum += shfl_xor(sum, 2);
+    sum += shfl_xor(sum, 4);
+    if (part == 0) {
+      a.delta[row[p]] = sum;
+      a.delta[(int64_t)a.bh * rows_bh + row[p]] = -lse[p] / a.scale;
+    }
+  }
+}
 
-
-// Key groups of up to 1024 queries' tiles (n <= 1024) run the SEQ schedule at
-// three waves per SIMD, longer ones the interleaved one at two: measured
-// (dK/dV, caches evicted) 73.4 vs 76.4 us at B=8, n=1024, bs 16; 76.5 vs 80.9
-// at bs 256; 41.9 vs 45.0 at B=32, n=256; equal at n=512 and at n=1024, bs 4;
-// but 128.3 vs 121.5 us at B=4, n=2048, bs 16 and 136.9 vs 124.7 at bs 4.
-template <bool MASK16>
-void launch_dkdv(const BwdArgs& a, dim3 grid, dim3 block, hipStream_t stream) {
-  if (a.n <= 1024)
-    hipLaunchKernelGGL((attn_bwd_dkdv_dma_kernel<3, MASK16, true>), grid, block, 0, stream, a);
+// The backward's work items in one launch: dQ query tiles and dK/dV key
+// tiles of every batch*head, in the host's order (a.order, longest first,
+// the two kinds interleaved), batch*head the fastest grid axis so that a
+// head's items share one XCD and its L2. Both kinds only read the Delta
+// pass's planes, so they need no ordering between them, and one launch has
+// one start-up and one tail instead of two. One LDS buffer serves either
+// kind's ring.
+template <int OCC, bool MASK16, bool SEQ>
+__global__ __launch_bounds__(256, OCC) void attn_bwd_kernel(BwdArgs a) {
+  __shared__ __attribute__((aligned(1024))) __bf16 smem[kBwdLdsBytes / 2];
+  const int id = wg_x();
+  const int slot = id / a.bh, bh = id - slot * a.bh;
+  const int code = a.n_items <= kBwdOrderMax ? (int)a.order[slot] : a.first_code + slot;
+  const int dq_items = 2 * a.n / 128;
+  const int dk_rank = code - dq_items;
+  if (code < dq_items)
+    dq_item<MASK16>(a, smem, bh, code);
+  else if (dk_rank >= a.n / 128 && 32 % a.bs == 0)  // a noisy key tile, blocks within 32 keys
+    dkdv_item<MASK16, SEQ, true>(a, smem, bh, dk_rank);
   else
-    hipLaunchKernelGGL((attn_bwd_dkdv_dma_kernel<2, MASK16, false>), grid, block, 0, stream, a);
+    dkdv_item<MASK16, SEQ, false>(a, smem, bh, dk_rank);
 }
 
 }  // namespace
 
-hipError_t launch_attn_bwd_dq(const BwdArgs& a, hipStream_t stream) {
-  // n % 128 == 0 always holds (validated): 128-row query tiles of 4 waves.
-  const dim3 grid(a.bh * (2 * a.n / 128)), block(256);
-  if (a.bs % 16 == 0)
-    hipLaunchKernelGGL((attn_bwd_dq_dma_kernel<BD3_DQ_OCC, true>), grid, block, 0, stream, a);
-  else
-    hipLaunchKernelGGL((attn_bwd_dq_dma_kernel<BD3_DQ_OCC, false>), grid, block, 0, stream, a);
+hipError_t launch_attn_bwd_delta(const BwdArgs& a, hipStream_t stream) {
+  // 128 rows per workgroup; batch * heads * 2n is a multiple of 256.
+  const int64_t rows = (int64_t)a.bh * 2 * a.n;
+  hipLaunchKernelGGL(attn_bwd_delta_kernel, dim3((unsigned)(rows / 128)), dim3(256), 0, stream, a);
   return hipGetLastError();
 }
 
-hipError_t launch_attn_bwd_dkdv(const BwdArgs& a, hipStream_t stream) {
-  // 128-key tiles of 4 waves.
-  const dim3 grid(a.bh * (2 * a.n / 128)), block(256);
+hipError_t launch_attn_bwd_items(const BwdArgs& a, hipStream_t stream) {
+  // One 4-wave workgroup per (item, batch*head); three per CU (168 VGPRs,
+  // 51 KB of LDS). dK/dV items run the SEQ schedule (one 32-row block at a
+  // time), which fits three waves per SIMD next to the dQ items.
+  const dim3 grid(a.bh * a.n_items), block(256);
   if (a.bs % 16 == 0)
-    launch_dkdv<true>(a, grid, block, stream);
+    hipLaunchKernelGGL((attn_bwd_kernel<3, true, true>), grid, block, 0, stream, a);
   else
-    launch_dkdv<false>(a, grid, block, stream);
+    hipLaunchKernelGGL((attn_bwd_kernel<3, false, true>), grid, block, 0, stream, a);
   return hipGetLastError();
 }
 

@@ -9,6 +9,7 @@
 namespace bd3 {
 
 constexpr int kHeadDim = 64;
+constexpr int kBwdOrderMax = 256;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
@@ -40,7 +41,14 @@ struct BwdArgs {
   uint16_t* dq;
   uint16_t* dk;
   uint16_t* dv;
-  float* delta;  // (B, H, 2n) fp32: written by the dQ kernel, read by dK/dV
+  float* delta;  // 2 x (B, H, 2n) fp32: Delta, then -L / scale (the Delta pass writes both)
+  // Work items of one batch*head, in launch order (host built, longest
+  // first): code c < 2n/128 is dQ query tile c, otherwise dK/dV key tile
+  // c - 2n/128 (see attn_bwd.hip). With more than kBwdOrderMax items the
+  // codes run first_code, first_code + 1, ... instead.
+  uint16_t order[256];
+  int n_items;
+  int first_code;
   Strides3 sq, sk, sv, so, sdo, sdq, sdk, sdv;
   int heads;
   int bh;
@@ -131,8 +139,10 @@ struct GlueArgs {
 };
 
 hipError_t launch_attn_fwd(const FwdArgs& a, hipStream_t stream);
-hipError_t launch_attn_bwd_dq(const BwdArgs& a, hipStream_t stream);
-hipError_t launch_attn_bwd_dkdv(const BwdArgs& a, hipStream_t stream);
+// The backward's Delta pass (Delta and -L / scale), then one launch of the
+// items in a.order (dQ and / or dK/dV).
+hipError_t launch_attn_bwd_delta(const BwdArgs& a, hipStream_t stream);
+hipError_t launch_attn_bwd_items(const BwdArgs& a, hipStream_t stream);
 hipError_t launch_decode(const DecodeArgs& a, int qt, hipStream_t stream);
 hipError_t launch_prefill(const DecodeArgs& a, hipStream_t stream);
 hipError_t launch_qkv_rope(const QkvRopeArgs& a, hipStream_t stream);

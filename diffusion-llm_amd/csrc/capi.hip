@@ -5,6 +5,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <algorithm>
 #include <cmath>
 #include <mutex>
 #include <string>
@@ -127,6 +128,35 @@ bd3::BwdArgs bwd_args(const void* q, const void* k, const void* v, const void* o
   a.scale = scale;
   a.scale_log2 = scale * bd3::kLog2e;
   return a;
+}
+
+// The backward's work items of one batch*head in launch order, longest
+// first: a stable sort on each item's MFMA work, the tiles it walks times
+// the products per tile (a dQ query tile three: S, dP, dQ; a dK/dV key tile
+// four: S, dP, dV, dK). Codes as attn_bwd.hip reads them: c < 2n/128 is dQ
+// query tile c, otherwise dK/dV key tile c - 2n/128.
+void bwd_order(bd3::BwdArgs& a, bool dq, bool dkdv) {
+  const int r = 2 * a.n / 128;
+  a.first_code = dq ? 0 : r;
+  a.n_items = (dq ? r : 0) + (dkdv ? r : 0);
+  if (a.n_items > bd3::kBwdOrderMax) return;  // the kernel walks the codes in order
+  int cost[2 * bd3::kBwdOrderMax], codes[bd3::kBwdOrderMax];
+  for (int i = 0; i < a.n_items; ++i) {
+    const int c = a.first_code + i;
+    codes[i] = c;
+    if (c < r) {
+      const int q0 = ((c & 1) ? 0 : a.n) + (r / 2 - 1 - (c >> 1)) * 128;
+      const bd3::KeyRanges kr = bd3::train_key_ranges(q0, 128, a.n, a.bs, 64);
+      cost[c] = 3 * ((kr.t1 - kr.t0) + (kr.t3 - kr.t2));
+    } else {
+      const int kt = c - r;
+      const int k0 = kt < r / 2 ? a.n + kt * 128 : (kt - r / 2) * 128;
+      const bd3::KeyRanges qr = bd3::train_query_ranges(k0, 128, a.n, a.bs, 64);
+      cost[c] = 4 * ((qr.t1 - qr.t0) + (qr.t3 - qr.t2));
+    }
+  }
+  std::stable_sort(codes, codes + a.n_items, [&](int x, int y) { return cost[x] > cost[y]; });
+  for (int i = 0; i < a.n_items; ++i) a.order[i] = (uint16_t)codes[i];
 }
 
 // Above this many queries the decode call runs the prefill kernel (128-row
@@ -336,7 +366,10 @@ int bd3_attn_bwd_dq(const void* q, const void* k, const void* v, const void* o, 
   a.so = s3(strides + 9);
   a.sdo = s3(strides + 12);
   a.sdq = s3(strides + 15);
-  return hip_status(bd3::launch_attn_bwd_dq(a, static_cast<hipStream_t>(stream)), "attn_bwd_dq launch");
+  bwd_order(a, true, false);
+  if ((st = hip_status(bd3::launch_attn_bwd_delta(a, static_cast<hipStream_t>(stream)), "attn_bwd Delta launch")))
+    return st;
+  return hip_status(bd3::launch_attn_bwd_items(a, static_cast<hipStream_t>(stream)), "attn_bwd_dq launch");
 }
 
 int bd3_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* dout, const float* lse,
@@ -361,8 +394,52 @@ int bd3_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* d
   a.sdo = s3(strides + 9);
   a.sdk = s3(strides + 12);
   a.sdv = s3(strides + 15);
-  return hip_status(bd3::launch_attn_bwd_dkdv(a, static_cast<hipStream_t>(stream)),
-                    "attn_bwd_dkdv launch");
+  bwd_order(a, false, true);
+  return hip_status(bd3::launch_attn_bwd_items(a, static_cast<hipStream_t>(stream)), "attn_bwd_dkdv launch");
+}
+
+int bd3_attn_bwd_delta(const void* o, const void* dout, const float* lse, float* delta, int32_t batch,
+                       int32_t heads, int32_t n, int32_t head_dim, int32_t block_size, const int64_t* strides,
+                       float scale, void* stream) {
+  int st = check_bwd_shape(batch, heads, n, head_dim, block_size, strides);
+  if (st) return st;
+  if ((st = check_scale(scale))) return st;
+  const char* names[2] = {"o", "dout"};
+  const void* ptrs[2] = {o, dout};
+  for (int i = 0; i < 2; ++i)
+    if ((st = check_tensor(ptrs[i], strides + 3 * i, names[i]))) return st;
+  if (lse == nullptr || delta == nullptr) return fail(BD3_EINVAL, "lse and delta must be non-NULL");
+  bd3::BwdArgs a = bwd_args(nullptr, nullptr, nullptr, o, dout, lse, nullptr, nullptr, nullptr, delta, batch, heads,
+                            n, block_size, scale);
+  a.so = s3(strides);
+  a.sdo = s3(strides + 3);
+  return hip_status(bd3::launch_attn_bwd_delta(a, static_cast<hipStream_t>(stream)), "attn_bwd Delta launch");
+}
+
+int bd3_attn_bwd_main(const void* q, const void* k, const void* v, const void* dout, const float* lse,
+                      const float* delta, void* dq, void* dk, void* dv, int32_t batch, int32_t heads, int32_t n,
+                      int32_t head_dim, int32_t block_size, const int64_t* strides, float scale, void* stream) {
+  int st = check_bwd_shape(batch, heads, n, head_dim, block_size, strides);
+  if (st) return st;
+  if ((st = check_scale(scale))) return st;
+  const char* names[7] = {"q", "k", "v", "dout", "dq", "dk", "dv"};
+  const void* ptrs[7] = {q, k, v, dout, dq, dk, dv};
+  for (int i = 0; i < 7; ++i)
+    if ((st = check_tensor(ptrs[i], strides + 3 * i, names[i]))) return st;
+  for (int i : {0, 1, 2, 3})
+    if ((st = check_dma_stride(strides + 3 * i, names[i]))) return st;
+  if (lse == nullptr || delta == nullptr) return fail(BD3_EINVAL, "lse and delta must be non-NULL");
+  bd3::BwdArgs a = bwd_args(q, k, v, nullptr, dout, lse, dq, dk, dv, const_cast<float*>(delta), batch, heads, n,
+                            block_size, scale);
+  a.sq = s3(strides);
+  a.sk = s3(strides + 3);
+  a.sv = s3(strides + 6);
+  a.sdo = s3(strides + 9);
+  a.sdq = s3(strides + 12);
+  a.sdk = s3(strides + 15);
+  a.sdv = s3(strides + 18);
+  bwd_order(a, true, true);
+  return hip_status(bd3::launch_attn_bwd_items(a, static_cast<hipStream_t>(stream)), "attn_bwd launch");
 }
 
 int bd3_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
@@ -385,18 +462,17 @@ int bd3_attn_bwd(const void* q, const void* k, const void* v, const void* o, con
   const size_t need = bd3_attn_bwd_workspace_bytes(batch, heads, n, head_dim);
   if (workspace == nullptr || !aligned16(workspace) || workspace_bytes < need)
     return fail(BD3_EINVAL, "workspace must be a 16-byte aligned buffer of >= %zu bytes", need);
-  // q, k, v, o, dout, dq | q, k, v, dout, dk, dv
-  const int64_t* S = strides;
-  const int64_t dq_strides[18] = {S[0],  S[1],  S[2],  S[3],  S[4],  S[5],  S[6],  S[7],  S[8],
-                                  S[9],  S[10], S[11], S[12], S[13], S[14], S[15], S[16], S[17]};
-  const int64_t kv_strides[18] = {S[0],  S[1],  S[2],  S[3],  S[4],  S[5],  S[6],  S[7],  S[8],
-                                  S[12], S[13], S[14], S[18], S[19], S[20], S[21], S[22], S[23]};
+  // The Delta pass, then every dQ and dK/dV item in one launch.
   float* delta = static_cast<float*>(workspace);
-  st = bd3_attn_bwd_dq(q, k, v, o, dout, lse, dq, delta, batch, heads, n, head_dim, block_size,
-                       dq_strides, scale, stream);
-  if (st) return st;
-  return bd3_attn_bwd_dkdv(q, k, v, dout, lse, delta, dk, dv, batch, heads, n, head_dim, block_size,
-                           kv_strides, scale, stream);
+  const int64_t* S = strides;  // q, k, v, o, dout, dq, dk, dv
+  const int64_t delta_strides[6] = {S[9], S[10], S[11], S[12], S[13], S[14]};
+  const int64_t main_strides[21] = {S[0],  S[1],  S[2],  S[3],  S[4],  S[5],  S[6],  S[7],  S[8],  S[12], S[13],
+                                    S[14], S[15], S[16], S[17], S[18], S[19], S[20], S[21], S[22], S[23]};
+  if ((st = bd3_attn_bwd_delta(o, dout, lse, delta, batch, heads, n, head_dim, block_size, delta_strides, scale,
+                               stream)))
+    return st;
+  return bd3_attn_bwd_main(q, k, v, dout, lse, delta, dq, dk, dv, batch, heads, n, head_dim, block_size,
+                           main_strides, scale, stream);
 }
 
 }  // extern "C"
@@ -803,10 +879,16 @@ int bd3_train_tile_census(int32_t n, int32_t block_size, int64_t* out) {
           if (live) exec_rows += 32 * 64;
         }
   }
-  // Key-stationary schedule (dK/dV kernel): 128-key workgroups visit the
+  // Key-stationary schedule (dK/dV items): 128-key workgroups visit the
   // 64-row tiles of train_query_ranges; each 32-key wave computes both 32-row
-  // halves of a tile when either holds a live pair for its keys.
+  // halves of a tile when either holds a live pair for its keys. A noisy key
+  // tile with block size dividing 32 computes each wave's diagonal 32 x 32
+  // block only.
   for (int k0 = 0; k0 < 2 * n; k0 += 128) {
+    if (k0 < n && 32 % block_size == 0) {
+      exec_keys += 4 * 32 * 32;
+      continue;
+    }
     const bd3::KeyRanges qr = bd3::train_query_ranges(k0, 128, n, block_size, 64);
     const int ranges[2][2] = {{qr.t0, qr.t1}, {qr.t2, qr.t3}};
     for (int rg = 0; rg < 2; ++rg)

@@ -36,6 +36,9 @@ SIGNATURES: dict[str, tuple] = {
                                     _i32, _i32, _i32, _i32, _i32, _i64p, _f32, _c_p]),
     "bd3_attn_bwd_noalloc": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _i32, _i32,
                                             _i32, _i32, _i32, _i64p, _f32, _c_p]),
+    "bd3_attn_bwd_delta": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i64p, _f32, _c_p]),
+    "bd3_attn_bwd_main": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _i32, _i32, _i32,
+                                         _i32, _i32, _i64p, _f32, _c_p]),
     "bd3_attn_bwd_dq": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _i32, _i32, _i32,
                                        _i32, _i32, _i64p, _f32, _c_p]),
     "bd3_attn_bwd_dkdv": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _i32, _i32, _i32,

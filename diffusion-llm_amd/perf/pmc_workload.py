@@ -6,7 +6,8 @@ Dispatches, in order and each `--reps` times:
   1. a plain device copy of --copy-mib MiB (torch copy_) - the calibration
      kernel: its FETCH_SIZE / WRITE_SIZE per dispatch against its known
      byte count gives the factor that turns the counters into bytes;
-  2. the training forward, dQ and dK/dV kernels, by default at BASELINE
+  2. the training forward and the backward (its Delta pass and its main
+     launch of every dQ and dK/dV item), by default at BASELINE
      configs[1] (B=8, L=1024, H=12, d=64, block 16, bf16; --batch, --heads,
      --seq-len and --block-size change the shape);
   3. the split-KV decode at configs[3] (32 x 12 heads, q_len 16,
@@ -67,8 +68,7 @@ def main(argv=None) -> int:
     step = TrainStep(args.batch, args.heads, args.seq_len, args.block_size, dev)
     for _ in range(args.reps):
         step.fwd()
-        step.bwd_dq()
-        step.bwd_dkdv()
+        step.bwd()
     torch.cuda.synchronize()
     print("training kernels done", flush=True)
     del step

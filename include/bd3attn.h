@@ -46,8 +46,9 @@ extern "C" {
 #define BD3_EHIP 2
 
 /* 2: bd3_train_tile_census writes 8 values (out[1] and out[6], out[7] are
- * the executed pairs of each kernel) and the second workspace plane of the
- * backward holds -L / scale. */
+ * the executed pairs of each kernel), the second workspace plane of the
+ * backward holds -L / scale, and bd3_attn_bwd_delta / bd3_attn_bwd_main
+ * split the backward into its Delta pass and one main launch. */
 #define BD3_ABI_VERSION 2
 
 /* Version of this ABI (BD3_ABI_VERSION). No reference counterpart. */
@@ -85,8 +86,9 @@ size_t bd3_attn_bwd_workspace_bytes(int32_t batch, int32_t heads, int32_t n,
 
 /*
  * Training attention backward: dQ, dK, dV of the forward above, given
- * dO and the forward's O and lse. Runs bd3_attn_bwd_dq then
- * bd3_attn_bwd_dkdv with Delta and -L / scale in the workspace.
+ * dO and the forward's O and lse: bd3_attn_bwd_delta (Delta and -L / scale
+ * into the workspace) then bd3_attn_bwd_main (every dQ and dK/dV work item
+ * in one launch).
  * strides: 24 int64 = (b, h, s) element strides of
  *          q, k, v, o, dout, dq, dk, dv.
  * Preconditions: as the forward, plus n % block_size == 0 (the reference
@@ -102,6 +104,40 @@ int bd3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
                  int32_t batch, int32_t heads, int32_t n, int32_t head_dim,
                  int32_t block_size, const int64_t* strides, float scale,
                  void* stream);
+
+/*
+ * Backward, Delta pass: Delta = rowsum(dO * O) and minus the forward's L
+ * over scale, written to `delta`: fp32, contiguous (2, batch, heads, 2n),
+ * plane 0 Delta, plane 1 -L / scale (the first bd3_attn_bwd_workspace_bytes()
+ * bytes of the backward workspace).
+ * strides: 6 int64 = (b, h, s) element strides of o, dout.
+ * Preconditions: as bd3_attn_bwd.
+ *
+ * Replaces the Delta torch op (kernels/BlockSparseFlashAttention.py:525).
+ */
+int bd3_attn_bwd_delta(const void* o, const void* dout, const float* lse,
+                       float* delta, int32_t batch, int32_t heads, int32_t n,
+                       int32_t head_dim, int32_t block_size,
+                       const int64_t* strides, float scale, void* stream);
+
+/*
+ * Backward, main launch: dQ = scale * dS K, dV = P^T dO and dK = scale *
+ * dS^T Q from the planes bd3_attn_bwd_delta wrote to `delta`; `lse` is
+ * checked but not read (the kernel uses the plane). One launch holds every
+ * query-stationary dQ item and key-stationary dK/dV item, longest first.
+ * strides: 21 int64 = (b, h, s) element strides of q, k, v, dout, dq, dk, dv.
+ * Preconditions: as bd3_attn_bwd.
+ *
+ * Replaces block_sparse_attention_bwd_dq_kern and
+ * block_sparse_attention_dk_dv_bwd_kern with their launches
+ * (kernels/BlockSparseFlashAttention.py:212-452, :532-560).
+ */
+int bd3_attn_bwd_main(const void* q, const void* k, const void* v,
+                      const void* dout, const float* lse, const float* delta,
+                      void* dq, void* dk, void* dv, int32_t batch,
+                      int32_t heads, int32_t n, int32_t head_dim,
+                      int32_t block_size, const int64_t* strides, float scale,
+                      void* stream);
 
 /*
  * bd3_attn_bwd without a workspace argument: the same kernels and results
@@ -129,10 +165,10 @@ int bd3_attn_bwd_noalloc(const void* q, const void* k, const void* v,
                          float scale, void* stream);
 
 /*
- * Backward, first stage: dQ = scale * dS K with dS = P o (dP - Delta),
- * and, for the second stage, Delta = rowsum(dO * O) and minus the
- * forward's L over scale written to `delta`: fp32, contiguous (2, batch,
- * heads, 2n), plane 0 Delta, plane 1 -L / scale.
+ * Backward in two stages (the reference's two kernels): first stage = the
+ * Delta pass (bd3_attn_bwd_delta) and the dQ items, dQ = scale * dS K with
+ * dS = P o (dP - Delta); the planes go to `delta`: fp32, contiguous (2,
+ * batch, heads, 2n), plane 0 Delta, plane 1 -L / scale.
  * strides: 18 int64 = (b, h, s) element strides of q, k, v, o, dout, dq.
  * Preconditions: as bd3_attn_bwd.
  *
@@ -146,9 +182,10 @@ int bd3_attn_bwd_dq(const void* q, const void* k, const void* v,
                     const int64_t* strides, float scale, void* stream);
 
 /*
- * Backward, second stage: dV = P^T dO and dK = scale * dS^T Q, given the
- * two planes (Delta, -L / scale) the first stage wrote to `delta`; `lse`
- * is checked but not read (the kernel uses the plane).
+ * Backward, second stage: the dK/dV items, dV = P^T dO and dK = scale *
+ * dS^T Q, given the two planes (Delta, -L / scale) the first stage wrote to
+ * `delta`; `lse` is checked but not read (the kernel uses the plane).
+ * bd3_attn_bwd runs both stages' items in one launch instead.
  * strides: 18 int64 = (b, h, s) element strides of q, k, v, dout, dk, dv.
  * Preconditions: as bd3_attn_bwd.
  *

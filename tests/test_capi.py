@@ -54,8 +54,14 @@ def test_census_matches_oracle(lib, n, bs):
     # (32 rows x 64 keys) for the forward / dQ, (64 rows x 32 keys) for dK/dV
     rows = m.reshape(2 * n // 32, 32, 2 * n // 64, 64).any(axis=(1, 3))
     keys = m.reshape(2 * n // 64, 64, 2 * n // 32, 32).any(axis=(1, 3))
+    if 32 % bs == 0:  # noisy key tiles: each 32-key wave computes its diagonal 32 x 32 block only
+        diag = m[:n, :n].reshape(n // 32, 32, n // 32, 32).any(axis=(1, 3))
+        assert np.array_equal(diag, np.eye(n // 32, dtype=bool))
+        keys[:, : n // 32] = False
+        assert out[7] == 2048 * int(keys.sum()) + 1024 * (n // 32)
+    else:
+        assert out[7] == 2048 * int(keys.sum())
     assert out[1] == out[6] == 2048 * int(rows.sum())
-    assert out[7] == 2048 * int(keys.sum())
     assert out[1] >= 1024 * (out[2] + out[3]) >= out[0]
 
 
@@ -175,6 +181,23 @@ def test_bwd_validation(lib):
     expect_einval(lib.bd3_attn_bwd_dkdv(*[GOOD] * 8, 1, 1, 128, 64, 5, st18, 0.125, None), "block_size")
     expect_einval(lib.bd3_attn_bwd_dkdv(GOOD, GOOD, GOOD, GOOD + 8, *[GOOD] * 4, 1, 1, 128, 64, 16, st18,
                                         0.125, None), "dout")
+
+
+def test_bwd_stage_validation(lib):
+    """The Delta pass and the main launch refuse bad arguments before any
+    HIP call (fake device pointers)."""
+    st6, st21 = _i64([64 * 256, 64 * 256, 64] * 2), _i64([64 * 256, 64 * 256, 64] * 7)
+    expect_einval(lib.bd3_attn_bwd_delta(GOOD, GOOD, GOOD, None, 1, 1, 128, 64, 16, st6, 0.125, None), "delta")
+    expect_einval(lib.bd3_attn_bwd_delta(GOOD, GOOD + 8, GOOD, GOOD, 1, 1, 128, 64, 16, st6, 0.125, None), "dout")
+    expect_einval(lib.bd3_attn_bwd_delta(GOOD, GOOD, GOOD, GOOD, 1, 1, 100, 64, 16, st6, 0.125, None), "multiple of 128")
+    expect_einval(lib.bd3_attn_bwd_main(*[GOOD] * 5, None, *[GOOD] * 3, 1, 1, 128, 64, 16, st21, 0.125, None), "delta")
+    expect_einval(lib.bd3_attn_bwd_main(*[GOOD] * 9, 1, 1, 128, 64, 5, st21, 0.125, None), "block_size")
+    bad = [64 * 256, 64 * 256, 64] * 7
+    bad[3 * 3 + 2] = 1 << 24  # dout's sequence stride: loaded tile by tile
+    expect_einval(lib.bd3_attn_bwd_main(*[GOOD] * 9, 1, 1, 128, 64, 16, _i64(bad), 0.125, None), "dout sequence stride")
+    for scale in (0.0, float("nan")):
+        expect_einval(lib.bd3_attn_bwd_delta(*[GOOD] * 4, 1, 1, 128, 64, 16, st6, scale, None), "scale")
+        expect_einval(lib.bd3_attn_bwd_main(*[GOOD] * 9, 1, 1, 128, 64, 16, st21, scale, None), "scale")
 
 
 def test_bwd_refuses_before_any_launch(lib):
