@@ -7,32 +7,34 @@
 //   P  = exp(S*scale - L)            (S = Q K^T, L the forward's lse)
 //   dV = P^T dO,  dP = dO V^T,  dS = P o (dP - Delta),  Delta = rowsum(dO o O)
 //   dK = scale * dS^T Q,  dQ = scale * dS K
-// Like the reference, two kernels: one owns query rows and forms dQ, the
-// other owns keys and forms dK, dV; both recompute S and dP. Neither needs
-// atomics or a transposed copy of dS, and results are deterministic.
+// Two launches. attn_bwd_delta_kernel forms Delta = rowsum(dO o O) (the
+// reference's separate op) and each row's -L / scale. attn_bwd_kernel then
+// runs every work item of the reference's two kernels in one launch: dQ
+// items own query rows and form dQ, dK/dV items own keys and form dK, dV;
+// both recompute S and dP. Neither kind needs atomics or a transposed copy
+// of dS, results are deterministic, and as both kinds only read the Delta
+// pass's planes the launch orders them freely: longest first (a host-built
+// table), so it has one start-up and one tail.
 //
-// attn_bwd_dq_dma_kernel (query-stationary, the forward's schedule): 4 waves
-//   of 32 rows. Q and dO rows live in registers as B operands; K, V key tiles
-//   come through LDS. S^T = K Q^T and dP^T = V dO^T put one row per lane, so
-//   L and Delta are per-lane scalars; dQ^T += K^T dS^T reads K^T from the LDS
-//   tile with ds_read_b64_tr_b16. Delta = rowsum(dO o O) is formed here from
-//   the row registers and stored for the second kernel (this fuses the
-//   reference's separate Delta op), next to the rows' -L / scale, the
-//   second kernel's score-chain seed.
-// attn_bwd_dkdv_dma_kernel (key-stationary): 4 waves of 32 keys. K and V rows
-//   live in registers as B operands of S = Q K^T and dP = dO V^T, which put
-//   one key per lane; query tiles (Q, dO, -L / scale, Delta) come through LDS.
+// dq_item (query-stationary, the forward's schedule): 4 waves of 32 rows. Q
+//   and dO rows live in registers as B operands; K, V key tiles come through
+//   LDS. S^T = K Q^T and dP^T = V dO^T put one row per lane, so L and Delta
+//   are per-lane scalars; dQ^T += K^T dS^T reads K^T from the LDS tile with
+//   ds_read_b64_tr_b16.
+// dkdv_item (key-stationary): 4 waves of 32 keys. K and V rows live in
+//   registers as B operands of S = Q K^T and dP = dO V^T, which put one key
+//   per lane; query tiles (Q, dO, -L / scale, Delta) come through LDS.
 //   dV += P^T dO and dK += dS^T Q take P^T / dS^T straight from registers and
-//   dO / Q transposed from LDS. dK, dV are written through LDS as 16-byte rows.
-//   Two schedules of the same arithmetic: the two 32-row blocks of a query
-//   tile one after the other at 3 waves per SIMD (n <= 1024), or their four
-//   product chains interleaved at 2 waves (longer rows).
+//   dO / Q transposed from LDS; the two 32-row blocks of a tile run one after
+//   the other, so three waves fit a SIMD next to the dQ items. dK, dV are
+//   written through LDS as 16-byte rows.
 // Every score is the exact fp32 dot product of the bf16 rows; scale and
 // log2(e) are applied in fp32 (dQ: one FMA per element; dK/dV: the chain
 // starts from -L / scale and the result is multiplied by scale * log2(e)).
-// Both load their tiles global -> LDS with global_load_lds into three-stage
-// rings of swizzled tiles (bd3_swz.h), two tiles ahead, with one counted
-// vmcnt wait and barrier per tile.
+// Both item kinds load their tiles global -> LDS with global_load_lds into
+// three-stage rings of swizzled tiles (bd3_swz.h), two tiles ahead, with one
+// counted vmcnt wait and barrier per tile, in one LDS buffer of the larger
+// ring's size.
 #include "bd3_device.h"
 #include "bd3_launch.h"
 #include "bd3_mask.h"
@@ -49,12 +51,11 @@ namespace {
 // ---------------------------------------------------------------------------
 // Key-stationary dK/dV. The query tiles (Q, dO and the rows' L and Delta) go
 // global -> LDS with global_load_lds into a three-stage ring of swizzled
-// tiles, two tiles ahead. Every live tile runs one code path over both of its 32-row
-// blocks; a block that is not fully visible to the wave's keys is masked in
-// place (MASK16: block size a multiple of 16, two tests per lane).
-// SEQ: the two 32-row blocks of a tile one after the other (a scheduling
-// barrier between them), so one block's chains are live at a time and three
-// waves fit a SIMD; otherwise their four chains are interleaved at two waves.
+// tiles, two tiles ahead. Every live tile runs one code path over both of its
+// 32-row blocks, one after the other (a scheduling barrier between them, so
+// one block's chains are live at a time); a block that is not fully visible
+// to the wave's keys is masked in place (MASK16: block size a multiple of 16,
+// two tests per lane).
 // Stage layout of the dK/dV ring (bytes): Q tile [0, 8K), dO tile [8K, 16K),
 // row scalars [16K, 17K): -L / scale of the 64 rows, then Delta, then both
 // again (the load that fetches them writes 1 KB).
@@ -106,7 +107,7 @@ __device__ __forceinline__ void dkdv_store(const BwdArgs& a, __bf16* smem, int b
 // are its own 128 rows: wave w's keys are seen only by the rows of 32-row
 // block w % 2 of tile w / 2, so each wave computes that one block (exactly
 // what the tile loop accumulates; its other blocks contribute zeros).
-template <bool MASK16, bool SEQ, bool DIAG>
+template <bool MASK16, bool DIAG>
 __device__ __forceinline__ void dkdv_item(const BwdArgs& a, __bf16* smem, int bh, int rank) {
   constexpr int kBK = 128;  // keys per workgroup: 4 waves x 32
   constexpr int kStages = kDkdvStages;
@@ -203,34 +204,10 @@ __device__ __forceinline__ void dkdv_item(const BwdArgs& a, __bf16* smem, int bh
 
   f32x16 dk[2] = {}, dv[2] = {};  // [d block]: lane = d column, registers = keys
 
-  // Scores and Delta - dP of the 32-row blocks of the current query tile
-  // (rows x keys, lane = key column, register r <-> row 32qb + 8(r/4) + 4g +
-  // r%4): the chains start from the rows' -L / scale and Delta, read from the
-  // tile's row scalars in accumulator order. The two blocks' four chains are
-  // issued interleaved, so no product waits for the one before it.
-  auto products = [&](const __bf16* qs, const __bf16* dos, const float* scal, f32x16 (&s)[2], f32x16 (&dp)[2]) {
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-      for (int rg = 0; rg < 4; ++rg) {
-        const f32x4 dr = *reinterpret_cast<const f32x4*>(&scal[64 + 32 * qb + 8 * rg + 4 * g]);
-        const f32x4 lr = *reinterpret_cast<const f32x4*>(&scal[32 * qb + 8 * rg + 4 * g]);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          dp[qb][4 * rg + j] = dr[j];
-          s[qb][4 * rg + j] = lr[j];
-        }
-      }
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        s[qb] = mfma32(sw_row_op(qs, 32 * qb, c, lane), kreg[c], s[qb]);     // S - L / scale
-        dp[qb] = mfma32(sw_row_op(dos, 32 * qb, c, lane), vreg[c], dp[qb]);  // Delta - dP (V negated)
-      }
-  };
-
-  // The same for one 32-row block qb (the SEQ schedule).
+  // Scores and Delta - dP of 32-row block qb of the current query tile (rows
+  // x keys, lane = key column, register r <-> row 32qb + 8(r/4) + 4g + r%4):
+  // the chains start from the rows' -L / scale and Delta, read from the
+  // tile's row scalars in accumulator order.
   auto block_products = [&](const __bf16* qs, const __bf16* dos, const float* scal, int qb, f32x16& s,
                             f32x16& dp) {
 #pragma unroll
@@ -326,43 +303,23 @@ __device__ __forceinline__ void dkdv_item(const BwdArgs& a, __bf16* smem, int bh
       const __bf16* qs = &smem[cur * (kStageBytes / 2)];
       const __bf16* dos = qs + kSwTile;
       const float* scal = reinterpret_cast<const float*>(qs + 2 * kSwTile);
-      if constexpr (SEQ) {
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-          f32x16 sc, dpc;
-          block_products(qs, dos, scal, qb, sc, dpc);
-          bf16x8 pop[2], dsop[2];  // [16-row step]
-          softmax_ops(sc, dpc, q0, qb, (qb ? c1 : c0) != kFull, pop, dsop);
-          // dV += P^T dO, dK += dS^T Q with dO / Q read transposed.
-#pragma unroll
-          for (int kc = 0; kc < 2; ++kc)
-#pragma unroll
-            for (int db = 0; db < 2; ++db) {
-              const bf16x8 dot = sw_tr_op(dos, 32 * qb + 16 * kc, 32 * db, lane);
-              const bf16x8 qt = sw_tr_op(qs, 32 * qb + 16 * kc, 32 * db, lane);
-              dv[db] = mfma32(pop[kc], dot, dv[db]);
-              dk[db] = mfma32(dsop[kc], qt, dk[db]);
-            }
-          if (qb == 0) __builtin_amdgcn_sched_barrier(0);
-        }
-      } else {
-        bf16x8 pop[2][2], dsop[2][2];  // [row block][16-row step]
-        f32x16 sc[2], dpc[2];
-        products(qs, dos, scal, sc, dpc);
-        softmax_ops(sc[0], dpc[0], q0, 0, c0 != kFull, pop[0], dsop[0]);
-        softmax_ops(sc[1], dpc[1], q0, 1, c1 != kFull, pop[1], dsop[1]);
+      for (int qb = 0; qb < 2; ++qb) {
+        f32x16 sc, dpc;
+        block_products(qs, dos, scal, qb, sc, dpc);
+        bf16x8 pop[2], dsop[2];  // [16-row step]
+        softmax_ops(sc, dpc, q0, qb, (qb ? c1 : c0) != kFull, pop, dsop);
         // dV += P^T dO, dK += dS^T Q with dO / Q read transposed.
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
+        for (int kc = 0; kc < 2; ++kc)
 #pragma unroll
-          for (int kc = 0; kc < 2; ++kc)
-#pragma unroll
-            for (int db = 0; db < 2; ++db) {
-              const bf16x8 dot = sw_tr_op(dos, 32 * qb + 16 * kc, 32 * db, lane);
-              const bf16x8 qt = sw_tr_op(qs, 32 * qb + 16 * kc, 32 * db, lane);
-              dv[db] = mfma32(pop[qb][kc], dot, dv[db]);
-              dk[db] = mfma32(dsop[qb][kc], qt, dk[db]);
-            }
+          for (int db = 0; db < 2; ++db) {
+            const bf16x8 dot = sw_tr_op(dos, 32 * qb + 16 * kc, 32 * db, lane);
+            const bf16x8 qt = sw_tr_op(qs, 32 * qb + 16 * kc, 32 * db, lane);
+            dv[db] = mfma32(pop[kc], dot, dv[db]);
+            dk[db] = mfma32(dsop[kc], qt, dk[db]);
+          }
+        if (qb == 0) __builtin_amdgcn_sched_barrier(0);
       }
     }
     wait_barrier(pf);
@@ -601,7 +558,7 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(BwdArgs a) {
 // pass's planes, so they need no ordering between them, and one launch has
 // one start-up and one tail instead of two. One LDS buffer serves either
 // kind's ring.
-template <int OCC, bool MASK16, bool SEQ>
+template <int OCC, bool MASK16>
 __global__ __launch_bounds__(256, OCC) void attn_bwd_kernel(BwdArgs a) {
   __shared__ __attribute__((aligned(1024))) __bf16 smem[kBwdLdsBytes / 2];
   const int id = wg_x();
@@ -612,9 +569,9 @@ __global__ __launch_bounds__(256, OCC) void attn_bwd_kernel(BwdArgs a) {
   if (code < dq_items)
     dq_item<MASK16>(a, smem, bh, code);
   else if (dk_rank >= a.n / 128 && 32 % a.bs == 0)  // a noisy key tile, blocks within 32 keys
-    dkdv_item<MASK16, SEQ, true>(a, smem, bh, dk_rank);
+    dkdv_item<MASK16, true>(a, smem, bh, dk_rank);
   else
-    dkdv_item<MASK16, SEQ, false>(a, smem, bh, dk_rank);
+    dkdv_item<MASK16, false>(a, smem, bh, dk_rank);
 }
 
 }  // namespace
@@ -628,13 +585,14 @@ hipError_t launch_attn_bwd_delta(const BwdArgs& a, hipStream_t stream) {
 
 hipError_t launch_attn_bwd_items(const BwdArgs& a, hipStream_t stream) {
   // One 4-wave workgroup per (item, batch*head); three per CU (168 VGPRs,
-  // 51 KB of LDS). dK/dV items run the SEQ schedule (one 32-row block at a
-  // time), which fits three waves per SIMD next to the dQ items.
+  // 51 KB of LDS). Measured against two waves per SIMD with the dK/dV
+  // items' four product chains interleaved (230 VGPRs): 258 vs 276 us at
+  // B=4, H=16, n=2048, 348 vs 380 at B=2, H=12, n=4096, 689 vs 746 at n=8192.
   const dim3 grid(a.bh * a.n_items), block(256);
   if (a.bs % 16 == 0)
-    hipLaunchKernelGGL((attn_bwd_kernel<3, true, true>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((attn_bwd_kernel<3, true>), grid, block, 0, stream, a);
   else
-    hipLaunchKernelGGL((attn_bwd_kernel<3, false, true>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((attn_bwd_kernel<3, false>), grid, block, 0, stream, a);
   return hipGetLastError();
 }
 
