@@ -64,7 +64,7 @@ struct DecodeArgs {
   const uint16_t* v;
   uint16_t* o;
   float* part_o;    // (BH, q_tiles, n_splits, QT, 64) fp32, or null
-  float* part_lse;  // (BH, q_tiles, n_splits, QT) natural log, or null
+  float* part_lse;  // (BH, q_tiles, n_splits, QT) log2 LSE, or null
   Strides3 sq, sk, sv, so;
   int heads;
   int bh;

@@ -17,8 +17,8 @@ def test_useful_flops_convention():
 
 
 def test_traffic_figures_are_committed():
-    for kernel in ("attn_fwd_dma_kernel", "attn_bwd_dq_dma_kernel", "attn_bwd_dkdv_dma_kernel",
-                   "decode16_partial"):
+    for kernel in ("attn_fwd_dma_kernel", "attn_bwd_delta_kernel", "attn_bwd_kernel", "decode16_partial",
+                   "qkv_rope_kernel", "ln_modulate_kernel"):
         t = bench.measured_traffic(kernel)
         assert isinstance(t, int) and t > 0, kernel
     assert bench.measured_traffic("no_such_kernel") is None

@@ -193,6 +193,56 @@ def test_batch1_profiling_shapes(cuda, record_error, shape, backend):
 
 
 @pytest.mark.gpu
+def test_cached_step_every_split_count(cuda, record_error):
+    """The reference's batch-1 cached shape at every split count 1-32 (one
+    partial per split, merged by decode_combine: 7-14 splits of 256-512 keys,
+    ragged last splits, 17-32 splits through the 32-split merge) against the
+    oracle; then 512 and 513 heads at two splits (q_len 9, block 7)."""
+    q, k, v = decode_inputs(1, 12, 16, 3584, seed=11)
+    ref = decode_attention(q, k, v, 16)
+    qd, kd, vd = (t.to(cuda, torch.bfloat16) for t in (q, k, v))
+    for ns in range(1, 33):
+        print(f"decode batch 1 x 12 heads, 3584 keys, {ns} splits", flush=True)
+        o = splitkv_capi(qd, kd, vd, 16, ns)
+        torch.cuda.synchronize()
+        record_error(f"decode O max-abs ({ns} splits)", max_abs(o, ref), OUT_TOL)
+    for B, H in ((32, 16), (27, 19)):
+        print(f"decode B={B} H={H} q_len 9 kv_len 300 2 splits", flush=True)
+        q, k, v = decode_inputs(B, H, 9, 300, seed=B + H)
+        o = splitkv_capi(*(t.to(cuda, torch.bfloat16) for t in (q, k, v)), 7, 2)
+        torch.cuda.synchronize()
+        record_error(f"decode O max-abs ({B * H} heads)", max_abs(o, decode_attention(q, k, v, 7)), OUT_TOL)
+
+
+@pytest.mark.gpu
+def test_cached_step_repeated_calls_on_two_streams(cuda):
+    """600 split-KV calls, three shapes alternating over two streams, 50 calls
+    in flight between synchronizations: every output equals its shape's first
+    one bit for bit (the split merge is deterministic and each call's partials
+    live in its own workspace)."""
+    shapes = [(1, 12, 16, 3584, 16, 16), (2, 3, 16, 300, 16, 5), (4, 12, 1, 1000, 4, 7)]
+    inputs, first = [], []
+    for i, (B, H, q_len, kv_len, bs, ns) in enumerate(shapes):
+        t = tuple(x.to(cuda, torch.bfloat16) for x in decode_inputs(B, H, q_len, kv_len, seed=90 + i))
+        inputs.append(t)
+        first.append(splitkv_capi(*t, bs, ns))
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    for batch in range(12):
+        print(f"repeated split-KV calls {50 * batch}..{50 * batch + 49}", flush=True)
+        outs = []
+        for i in range(50):
+            j = (50 * batch + i) % 3
+            with torch.cuda.stream(streams[i % 2]):
+                outs.append((j, splitkv_capi(*inputs[j], shapes[j][4], shapes[j][5])))
+        torch.cuda.synchronize()
+        for j, o in outs:
+            assert torch.equal(o, first[j]), f"shape {shapes[j]} differs in call batch {batch}"
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("q_len,kv_len,n_splits", [(1, 300, 1), (16, 700, 1), (16, 700, 3), (32, 1000, 2),
                                                    (300, 1100, 1), (300, 1100, 3)])
 def test_decode_scale_argument(cuda, q_len, kv_len, n_splits):
