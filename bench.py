@@ -15,8 +15,8 @@ bench/attention_bench.py:89,99, restricted to unmasked pairs).
 
 Printed on stdout as ONE JSON line, with:
   roofline      the dominant kernel's useful TFLOP/s against bf16 dense MFMA
-                peak (HIP events on the launch stream around back-to-back
-                launches of that kernel); traffic = its HBM bytes per launch from the committed
+                peak (the mean of HIP-event spans around that launch over K
+                steps of the same protocol); traffic = its HBM bytes per launch from the committed
                 rocprofv3 FETCH_SIZE / WRITE_SIZE summary
                 (profiles/hbm_traffic_pmc.md);
   cpu_baseline  the fp32 eager oracle's fwd+bwd (and fwd alone) on the host
@@ -183,10 +183,13 @@ def time_train(step: TrainStep, steps: int, warmup: int, use_graph: bool = False
     are evicted (a 1 GiB read, larger than the 256 MB Infinity Cache) before
     the forward and again before the backward, and HIP events on the launch
     stream (fence-free, perf.harness.StreamEvent) time each; fwd+bwd is their
-    sum. Events also separate the
-    backward's two kernels (dQ, dK/dV). With `use_graph` the forward and the
-    backward are replayed from two captured HIP graphs. The same steps are
-    also timed back to back without eviction (wall clock) for comparison.
+    sum. As in the reference, one pair of events brackets the whole backward
+    (an event between its two launches adds ~1.3 us of dispatch gap); the
+    split between the Delta pass and the main launch comes from `steps` more
+    steps of the same protocol with an event between them. With `use_graph`
+    the forward and the backward are replayed from two captured HIP graphs.
+    The same steps are also timed back to back without eviction (wall clock)
+    for comparison.
 
     Returns a dict: step_ms (median, p20, p80, mean of fwd + bwd over the
     timed steps), kernel_ms / kernel_mean_ms (median / mean of each kernel),
@@ -212,28 +215,35 @@ def time_train(step: TrainStep, steps: int, warmup: int, use_graph: bool = False
     events = []
     torch.cuda.synchronize()
     for _ in range(steps):
-        ev = [StreamEvent() for _ in range(5)]
+        ev = [StreamEvent() for _ in range(4)]
         flush_caches()
         ev[0].record(stream)
         fwd_fn()
         ev[1].record(stream)
         flush_caches()
         ev[2].record(stream)
-        if graphs is None:
-            step.bwd_delta()
-            ev[3].record(stream)
-            step.bwd_main()
-        else:
-            bwd_fn()
-            ev[3].record(stream)
-        ev[4].record(stream)
+        bwd_fn()
+        ev[3].record(stream)
         events.append(ev)
     torch.cuda.synchronize()
-    total = Samples([e[0].elapsed_time(e[1]) + e[2].elapsed_time(e[4]) for e in events])
-    spans = {"fwd": (0, 1), "bwd": (2, 4)}
+    total = Samples([e[0].elapsed_time(e[1]) + e[2].elapsed_time(e[3]) for e in events])
+    per = {k: Samples([e[a].elapsed_time(e[b]) for e in events]) for k, (a, b) in
+           {"fwd": (0, 1), "bwd": (2, 3)}.items()}
     if graphs is None:
-        spans.update(bwd_delta=(2, 3), bwd_main=(3, 4))
-    per = {k: Samples([e[a].elapsed_time(e[b]) for e in events]) for k, (a, b) in spans.items()}
+        # the backward's two launches apart: the same protocol, an event between them
+        split = []
+        for _ in range(steps):
+            ev = [StreamEvent() for _ in range(3)]
+            flush_caches()
+            ev[0].record(stream)
+            step.bwd_delta()
+            ev[1].record(stream)
+            step.bwd_main()
+            ev[2].record(stream)
+            split.append(ev)
+        torch.cuda.synchronize()
+        per["bwd_delta"] = Samples([e[0].elapsed_time(e[1]) for e in split])
+        per["bwd_main"] = Samples([e[1].elapsed_time(e[2]) for e in split])
     kernel_ms = {k: v.median_ms for k, v in per.items()}
     kernel_mean_ms = {k: v.mean_ms for k, v in per.items()}
     # the same steps back to back, caches warm, wall clock
