@@ -370,11 +370,16 @@ def decode_bench(device, reps: int):
                                        n_splits, st, 1.0 / 8, ptr(ws), nbytes, stream))
         return call
 
-    for ns in (1, 4, 8, 16, 0):
+    # At this shape (384 batch*heads) 2 or 3 splits write fp32 partials to HBM
+    # and merge them in a second launch (the reference's split_kv_kern +
+    # split_kv_reduce_kern); from 4 splits on one workgroup per head takes all
+    # of its splits and merges them on chip.
+    for ns in (1, 2, 3, 4, 8, 16, 0):
         eff = ns if ns else -(-kv_len // 256)  # 0: the reference's SPLIT_N = 256 rule
         t = bench(run(eff), warmup=5, rep=reps, flush=True)
+        merge = "none" if eff == 1 else ("partials in HBM + merge launch" if eff < 4 else "on chip, per head")
         rows.append({"n_splits": eff, "rule": "reference ceil(kv/256)" if ns == 0 else "explicit",
-                     "us": t.mean_ms * 1e3, "us_median": t.median_ms * 1e3,
+                     "merge": merge, "us": t.mean_ms * 1e3, "us_median": t.median_ms * 1e3,
                      "us_p20": t.p20_ms * 1e3, "us_p80": t.p80_ms * 1e3,
                      "GB_s": kv_bytes / (t.mean_ms * 1e-3) / 1e9})
     # the library's auto split (bd3_decode)
@@ -781,7 +786,8 @@ def main(argv=None) -> int:
     if not args.no_decode:
         result["decode"] = decode_bench(device, reps=30)
         for r in result["decode"]["rows"]:
-            log(f"decode n_splits={r['n_splits']:3d} ({r['rule']}): {r['us']:.1f} us, {r['GB_s']:.0f} GB/s")
+            log(f"decode n_splits={r['n_splits']:3d} ({r['rule']}, merge {r.get('merge', 'none')}): "
+                f"{r['us']:.1f} us, {r['GB_s']:.0f} GB/s")
     if not args.no_decode:
         result["decode_batch1"] = decode_b1_bench(device, reps=30)
         for k_, r in result["decode_batch1"].items():
