@@ -156,7 +156,7 @@ __device__ __forceinline__ void dkdv_item(const BwdArgs& a, __bf16* smem, int bh
     qoff[j] = (uint32_t)(2 * (r * (int)a.sq.s + ch));
     dooff[j] = (uint32_t)(2 * (r * (int)a.sdo.s + ch));
   }
-  // L comes as -L / scale, the second plane of the delta buffer (written by the dQ kernel).
+  // L comes as -L / scale, the second plane of the delta buffer (written by the Delta pass).
   const float* scal_src = ((lane & 16) ? a.delta : a.delta + (int64_t)a.bh * 2 * a.n) + rowbase + 4 * (lane & 15);
   const int64_t qstep = (int64_t)kSwRows * a.sq.s, dostep = (int64_t)kSwRows * a.sdo.s;
   const uint32_t lds0 = lds_addr(&smem[0]);

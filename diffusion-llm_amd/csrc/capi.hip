@@ -859,7 +859,7 @@ int bd3_train_tile_census(int32_t n, int32_t block_size, int64_t* out) {
     return fail(BD3_EINVAL, "need n a positive multiple of 128 and block_size >= 1");
   int64_t useful = 0, full = 0, partial = 0, skipped = 0, exec_rows = 0, exec_keys = 0;
   for (int q = 0; q < 2 * n; ++q) useful += bd3::train_row_keys(q, n, block_size);
-  // Query-stationary schedule (forward and dQ kernels): 128-row workgroups
+  // Query-stationary schedule (forward, dQ items): 128-row workgroups
   // visit the 64-key tiles of train_key_ranges; each 32-row wave computes
   // both 32-key halves of a tile when either holds a live pair for its rows.
   for (int q0 = 0; q0 < 2 * n; q0 += 128) {

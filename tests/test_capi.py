@@ -123,8 +123,8 @@ def test_walk_classes_match_mask(lib, n, bs, mode):
 
 @pytest.mark.parametrize("n,bs", [(8, 1), (8, 3), (64, 16), (96, 7), (128, 128), (256, 64)])
 def test_interval_forms_match_mask(lib, n, bs):
-    """The row intervals (forward, dQ kernels) and column intervals (dK/dV
-    kernel) reproduce every row and column of block_diff_mask."""
+    """The row intervals (forward, dQ items) and column intervals (dK/dV
+    items) reproduce every row and column of block_diff_mask."""
     m = block_diff_mask(n, bs)
     out = (ctypes.c_int32 * 4)()
     idx = np.arange(2 * n)
@@ -235,7 +235,7 @@ def test_scale_validation(lib, scale):
 
 def test_tile_load_offset_stride_limit(lib):
     """Sequence strides of the tensors the training kernels load tile by tile
-    (k, v in the forward and dQ kernels; q, dO in dK/dV) must keep the 32-bit
+    (k, v in the forward and the dQ items; q, dO in dK/dV) must keep the 32-bit
     per-lane load offsets in range: < 2^24 elements."""
     big = 1 << 24
     ok = [64 * 256, 64 * 256, 64]

@@ -10,11 +10,11 @@ weight (references: model/bd3lm.py:10-52, kernels/BlockSparseDecodeAttention.py:
   * forward: lse_i = ln(c_i), c_i the row's visible-key count, and
     O_i = mean of the visible V rows. With V_j one-hot on a bucket f(j),
     O_i[d] * c_i is the number of visible keys in bucket d (an integer).
-  * dQ kernel, fed lse = 0 and O = 0 (so Delta = 0), dO_i = e_0 and V_j all
+  * dQ stage, fed lse = 0 and O = 0 (so Delta = 0), dO_i = e_0 and V_j all
     ones: P = 1 and dS = 1 on visible pairs, so dQ_i = scale * sum of the
     visible K rows; with K_j one-hot on f(j), dQ_i[d] * 8 is an integer
     count (exact in bf16).
-  * dK/dV kernel, fed Delta = 0 and -L / scale = 0, K = 0, V_j all ones,
+  * dK/dV stage, fed Delta = 0 and -L / scale = 0, K = 0, V_j all ones,
     Q_i one-hot on g(i), dO_i one-hot on h(i): dV_j[d] counts the rows that
     see key j with h(i) = d, dK_j[d] * 8 those with g(i) = d (the transposed
     mask, exact integers).
