@@ -55,8 +55,11 @@ def rope_bf16(x_bits: np.ndarray, positions, sin: np.ndarray, cos: np.ndarray) -
     x = bf16_to_f32(x_bits)
     half = x.shape[-1] // 2
     x1, x2 = x[..., :half], x[..., half:]
-    out1 = _rnd(_rnd(x1 * c) - _rnd(x2 * s))
-    out2 = _rnd(_rnd(x1 * s) + _rnd(x2 * c))
+    # bf16 inputs near the format's maximum overflow to +-inf (and inf - inf
+    # gives NaN) exactly as torch's bf16 ops do; that is the expected result.
+    with np.errstate(over="ignore", invalid="ignore"):
+        out1 = _rnd(_rnd(x1 * c) - _rnd(x2 * s))
+        out2 = _rnd(_rnd(x1 * s) + _rnd(x2 * c))
     return bf16_bits(np.concatenate([out1, out2], axis=-1))
 
 

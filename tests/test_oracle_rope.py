@@ -26,15 +26,19 @@ def from_bits(b: np.ndarray) -> torch.Tensor:
 
 def test_bf16_rounding_matches_torch():
     rng = np.random.default_rng(0)
-    x = np.concatenate([
-        rng.standard_normal(100_000).astype(np.float32) * 10.0 ** rng.integers(-30, 30, 100_000),
-        # exact ties: bf16 value + half an ulp, both parities of the kept bit
-        (np.arange(1, 4097, dtype=np.uint32) << 16 | 0x8000).view(np.float32),
-        (np.arange(1, 4097, dtype=np.uint32) << 16 | 0x7FFF).view(np.float32),
-        np.array([0.0, -0.0, np.inf, -np.inf, 1e-40, -1e-40, 3.4e38, -3.4e38, np.nan, -np.nan],
-                 dtype=np.float32),
-        np.array([0x7F800001, 0xFFC12345, 0x7FBFFFFF], dtype=np.uint32).view(np.float32),  # NaN payloads
-    ])
+    # The concatenation is float64 (torch's float64 -> bf16 path, which
+    # canonicalises NaN to 0x7fc0 as its GPU conversion does); widening the
+    # signalling-NaN payloads below to float64 raises numpy's invalid flag.
+    with np.errstate(invalid="ignore"):
+        x = np.concatenate([
+            rng.standard_normal(100_000).astype(np.float32) * 10.0 ** rng.integers(-30, 30, 100_000),
+            # exact ties: bf16 value + half an ulp, both parities of the kept bit
+            (np.arange(1, 4097, dtype=np.uint32) << 16 | 0x8000).view(np.float32),
+            (np.arange(1, 4097, dtype=np.uint32) << 16 | 0x7FFF).view(np.float32),
+            np.array([0.0, -0.0, np.inf, -np.inf, 1e-40, -1e-40, 3.4e38, -3.4e38, np.nan, -np.nan],
+                     dtype=np.float32),
+            np.array([0x7F800001, 0xFFC12345, 0x7FBFFFFF], dtype=np.uint32).view(np.float32),  # NaN payloads
+        ])
     want = torch_bits(torch.from_numpy(x).to(torch.bfloat16))
     assert np.array_equal(bf16_bits(x), want)
 
