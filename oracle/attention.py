@@ -96,7 +96,8 @@ def bd3_attention_grads(q: Tensor, k: Tensor, v: Tensor, dout: Tensor, block_siz
 
 
 def bd3_attention_grads_rows(q: Tensor, k: Tensor, v: Tensor, dout: Tensor, block_size: int,
-                             rows: int = 1024) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+                             rows: int = 1024, delta_factor: float = 1.0
+                             ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     """(O, lse, dQ, dK, dV) of one (b, h) slice (tensors (S, d), fp32), the
     same values as bd3_attention / bd3_attention_grads with memory bounded to
     `rows` x S scores at a time: for long sequences (2n = 8192, 16384), where
@@ -107,7 +108,9 @@ def bd3_attention_grads_rows(q: Tensor, k: Tensor, v: Tensor, dout: Tensor, bloc
     P = softmax(S * scale + M) (M from model/bd3lm.py:10-52), O = P V cast as
     the reference casts P to v's dtype, Delta = rowsum(dO o O),
     dP = dO V^T, dS = P o (dP - Delta), dQ = scale dS K; dK += scale dS^T Q and
-    dV += P^T dO summed over the row blocks."""
+    dV += P^T dO summed over the row blocks. `delta_factor` multiplies Delta:
+    1 is the algorithm; tests pass another value to plant a mistake and show
+    that a property test catches it."""
     S, D = q.shape
     n = S // 2
     scale = 1.0 / D ** 0.5
@@ -124,7 +127,7 @@ def bd3_attention_grads_rows(q: Tensor, k: Tensor, v: Tensor, dout: Tensor, bloc
         lse[sl] = torch.logsumexp(s, dim=-1)
         p = softmax(s, dim=-1)
         o[sl] = torch.matmul(p.to(v.dtype), v)
-        delta = (dout[sl] * o[sl]).sum(-1, keepdim=True)
+        delta = (dout[sl] * o[sl]).sum(-1, keepdim=True) * delta_factor
         ds = p * (torch.matmul(dout[sl], v.transpose(-1, -2)) - delta)
         dq[sl] = torch.matmul(ds, k) * scale
         dk += torch.matmul(ds.transpose(-1, -2), q[sl]) * scale

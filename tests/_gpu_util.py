@@ -19,6 +19,19 @@ def train_inputs(B, H, n, seed=0, count=4, q_scale=1.0):
     return [bf16_round(t) for t in ts]
 
 
+def key_shift_inputs(B, H, n, seed=0):
+    """q, v, dO ~ N(0,1) rounded to bf16; keys on a 1/16 grid in [-4, 4] and
+    one shift vector c per (b, h) on the same grid in [-2, 2], so that k and
+    k + c are both exact in bf16 (every value a multiple of 1/16 below 8 in
+    magnitude). Returns q, k, v, dO (B, H, 2n, 64) and c (B, H, 1, 64)."""
+    g = torch.Generator().manual_seed(seed)
+    q, v, do = (bf16_round(torch.randn(B, H, 2 * n, D, generator=g)) for _ in range(3))
+    k = (torch.randn(B, H, 2 * n, D, generator=g) * 16).round().clamp(-64, 64) / 16
+    c = (torch.randn(B, H, 1, D, generator=g) * 8).round().clamp(-32, 32) / 16
+    assert torch.equal(bf16_round(k), k) and torch.equal(bf16_round(k + c), k + c)
+    return q, k, v, do, c
+
+
 def to_dev(ts, device):
     return [t.to(device=device, dtype=torch.bfloat16) for t in ts]
 

@@ -7,7 +7,7 @@ error; lse (natural log, what the forward saves) within 1e-2 abs.
 import pytest
 import torch
 
-from _gpu_util import bwd_capi, fwd_capi, max_abs, to_dev, train_inputs
+from _gpu_util import bwd_capi, fwd_capi, key_shift_inputs, max_abs, to_dev, train_inputs
 from kernels._native import check, lib, ptr, stream_of, strides
 from kernels.BlockSparseFlashAttention import BlockSparseFlashAttention
 from oracle.attention import bd3_attention, bd3_attention_grads, bd3_attention_grads_rows, rel_frobenius
@@ -163,6 +163,36 @@ def test_long_sequence(cuda, record_error, n, bs):
     dq, dk, dv = bwd_capi(qd, kd, vd, o, dod, lse, bs)
     torch.cuda.synchronize()
     check_slices(record_error, q, k, v, do, o, lse, dq, dk, dv, bs, ((0, 0), (B - 1, H - 1)), rows=1024)
+
+
+SHIFT = [(8, 12, 1024, 16), (1, 12, 8192, 16), (2, 12, 4096, 64), (2, 3, 640, 5)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,H,n,bs", SHIFT)
+def test_key_shift_invariance(cuda, record_error, B, H, n, bs):
+    """Every (b, h) slice at full size, no oracle: every key of a slice
+    shifted by one vector c (exactly: bf16-exact grid) moves each row's
+    scores by a constant, so O, dK and dV must not change, lse must move by
+    scale * q.c, and dQ moves by scale * (sum_j dS_ij) c, which the Delta pass
+    makes ~0 (a wrong Delta moves dQ by a large fraction of itself:
+    test_oracle_attention.py plants that mistake in the oracle)."""
+    print(f"key shift B={B} H={H} n={n} bs={bs}", flush=True)
+    q, k, v, do, c = key_shift_inputs(B, H, n, seed=n + bs)
+    qd, kd, vd, dod, ksd = to_dev((q, k, v, do, k + c), cuda)
+    o, lse = fwd_capi(qd, kd, vd, bs)
+    dq, dk, dv = bwd_capi(qd, kd, vd, o, dod, lse, bs)
+    o2, lse2 = fwd_capi(qd, ksd, vd, bs)
+    dq2, dk2, dv2 = bwd_capi(qd, ksd, vd, o2, dod, lse2, bs)
+    torch.cuda.synchronize()
+    qc = (q.to(cuda) * c.to(cuda)).sum(-1) / 8.0  # scale * q.c per row, fp32
+    record_error("shift: lse move - scale q.c max-abs", float((lse2 - lse - qc).abs().max()), LSE_TOL)
+    # P moves by fp32 rounding only; a bf16 ulp of O near 2 is 2^-7 (the output bar's half)
+    record_error("shift: O max-abs", float((o2.float() - o.float()).abs().max()), OUT_TOL)
+    for name, a, b in (("dQ", dq2, dq), ("dK", dk2, dk), ("dV", dv2, dv)):
+        a, b = a.float(), b.float()
+        rel = ((a - b).pow(2).sum((-1, -2)).sqrt() / b.pow(2).sum((-1, -2)).sqrt()).max()  # worst slice
+        record_error(f"shift: {name} rel-F (worst slice)", float(rel), 1e-2)
 
 
 @pytest.mark.gpu

@@ -120,6 +120,30 @@ def test_row_blocked_grads_equal_autograd(n, bs, rows):
         assert torch.allclose(got.double(), ref[0, 0].double(), rtol=1e-10, atol=1e-10)
 
 
+@pytest.mark.parametrize("n,bs", [(128, 16), (96, 1), (64, 64)])
+def test_key_shift_invariance_pins_delta(n, bs):
+    """Shifting every key of a slice by one vector c moves each row's scores
+    by a constant, so O, dK and dV stay and dQ moves by scale * (sum_j dS_ij) c,
+    which is 0 because Delta = rowsum(dO o O) makes every row of dS sum to 0.
+    The oracle (float64) keeps all four; with Delta planted wrong in the
+    oracle (zero or doubled) dQ moves by a large fraction of itself, so the
+    GPU property test over every slice (tests/test_gpu_train.py) detects a
+    wrong Delta without the oracle."""
+    from _gpu_util import key_shift_inputs
+    q, k, v, do, c = (t[0, 0].double() for t in key_shift_inputs(1, 1, n, seed=n + bs))
+    base = bd3_attention_grads_rows(q, k, v, do, bs, rows=64)
+    moved = bd3_attention_grads_rows(q, k + c, v, do, bs, rows=64)
+    scale = 1.0 / q.shape[-1] ** 0.5
+    rel = lambda a, b: float((a - b).norm() / b.norm())
+    assert torch.allclose(moved[1] - base[1], (q @ c[0]) * scale, atol=1e-9)  # lse moves by scale * q.c
+    for i in (0, 2, 3, 4):  # O, dQ, dK, dV
+        assert rel(moved[i], base[i]) < 1e-9
+    for factor in (0.0, 2.0):
+        planted = bd3_attention_grads_rows(q, k, v, do, bs, rows=64, delta_factor=factor)
+        planted_moved = bd3_attention_grads_rows(q, k + c, v, do, bs, rows=64, delta_factor=factor)
+        assert rel(planted_moved[2], planted[2]) > 0.1
+
+
 def test_cached_decode_step_is_unmasked_sdpa():
     q = rand(2, 3, 16, 8, seed=50)
     k, v = rand(2, 3, 160, 8, seed=51), rand(2, 3, 160, 8, seed=52)
