@@ -44,6 +44,38 @@ def test_bwd_matches_oracle(cuda, record_error, B, H, n, bs):
         record_error(f"{name} rel-F", rel_frobenius(got.cpu(), ref), GRAD_TOL)
 
 
+def _random_train_shapes(count: int, seed: int):
+    """(B, H, n, bs) from a fixed generator: n a multiple of 128 up to 768,
+    bs a divisor of n (odd ones included: per-element masks, MASK16 off), 1-2
+    sequences, 1-3 heads."""
+    import random
+    r = random.Random(seed)
+    out = []
+    for _ in range(count):
+        n = 128 * r.randint(1, 6)
+        divisors = [d for d in range(1, n + 1) if n % d == 0]
+        out.append((r.randint(1, 2), r.randint(1, 3), n, r.choice(divisors)))
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,H,n,bs", _random_train_shapes(12, seed=33))
+def test_train_random_shapes(cuda, record_error, B, H, n, bs):
+    """Forward and backward at seeded random shapes against the dense oracle."""
+    print(f"train random B={B} H={H} n={n} bs={bs}", flush=True)
+    q, k, v, do = train_inputs(B, H, n, seed=n + bs, count=4)
+    qd, kd, vd, dod = to_dev((q, k, v, do), cuda)
+    o, lse = fwd_capi(qd, kd, vd, bs)
+    dq, dk, dv = bwd_capi(qd, kd, vd, o, dod, lse, bs)
+    ro, rdq, rdk, rdv = bd3_attention_grads(q, k, v, do, bs)
+    _, rlse = bd3_attention(q, k, v, bs)
+    torch.cuda.synchronize()
+    record_error("O max-abs (random shapes)", max_abs(o, ro), OUT_TOL)
+    record_error("lse max-abs (random shapes)", max_abs(lse, rlse), LSE_TOL)
+    for name, got, ref in (("dQ", dq, rdq), ("dK", dk, rdk), ("dV", dv, rdv)):
+        record_error(f"{name} rel-F (random shapes)", rel_frobenius(got.cpu(), ref), GRAD_TOL)
+
+
 @pytest.mark.gpu
 def test_autograd_function_matches_capi(cuda):
     """The reference-shaped autograd Function gives the C-ABI results."""
