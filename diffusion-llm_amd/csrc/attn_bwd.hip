@@ -28,6 +28,13 @@
 //   dO / Q transposed from LDS; the two 32-row blocks of a tile run one after
 //   the other, so three waves fit a SIMD next to the dQ items. dK, dV are
 //   written through LDS as 16-byte rows.
+// Noisy key tiles with a block size dividing 32 (a noisy key is seen only by
+//   the noisy rows of its own block, so only the tile's diagonal 32 x 32
+//   blocks are live): in a launch with both kinds they get no dK/dV item;
+//   the dQ item of the same 128 rows walks its two diagonal key tiles last
+//   and, from their K / V still in the ring and its own Q / dO rows, forms
+//   those keys' dK and dV (diag_dkdv). Alone (the dK/dV stage), each such
+//   tile is an item whose waves compute only their diagonal block.
 // Every score is the exact fp32 dot product of the bf16 rows; scale and
 // log2(e) are applied in fp32 (dQ: one FMA per element; dK/dV: the chain
 // starts from -L / scale and the result is multiplied by scale * log2(e)).
@@ -329,6 +336,114 @@ __device__ __forceinline__ void dkdv_item(const BwdArgs& a, __bf16* smem, int bh
   dkdv_store(a, smem, bo.b, bo.h, kw, wave, lane, dk, dv);
 }
 
+// The dK and dV of the noisy keys with the same indices as a dQ item's wave's
+// 32 noisy rows (fold_diag: block sizes dividing 32). Such a key is seen only
+// by the noisy rows of its own block, all of them this wave's, so the wave's
+// 32 x 32 diagonal block gives the keys' whole dK and dV: the DIAG path of
+// dkdv_item on that one block. The dQ item walks its diagonal key tiles last,
+// so their K and V are still in the ring; the wave's Q and dO rows (held in
+// registers by the dQ item) are then staged into a wave-private swizzled
+// tile for the transposed operand reads. Every wave writes its own 32 keys
+// through its own LDS tile.
+template <bool MASK16>
+__device__ __forceinline__ void diag_dkdv(const BwdArgs& a, __bf16* smem, int b, int h, int qrow0, int wave, int lane,
+                                          const __bf16* ktile, const __bf16* vtile, const bf16x8 (&qreg)[4],
+                                          const bf16x8 (&doreg)[4], float lse_row, float drow) {
+  const int l32 = lane & 31;
+  const int g = lane >> 5;
+  const int key = qrow0 + l32;
+  // K rows and negated V rows of the wave's 32 keys: rows 32 (wave % 2) of
+  // the ring's K and V tiles of the diagonal tile, which the dQ loop visited
+  // last. Every wave holds them before the ring is reused for the staging.
+  bf16x8 kreg[4], vreg[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    kreg[c] = sw_row_op(ktile, 32 * (wave & 1), c, lane);
+    vreg[c] = __builtin_bit_cast(bf16x8, __builtin_bit_cast(u32x4, sw_row_op(vtile, 32 * (wave & 1), c, lane)) ^
+                                             0x80008000u);
+  }
+#pragma unroll
+  for (int c = 0; c < 4; ++c) asm volatile("" ::"v"(kreg[c]), "v"(vreg[c]));
+  __syncthreads();
+  // The wave's staging lies inside the LDS tile its dkdv_store uses (wave w:
+  // elements [w kTileElems, (w + 1) kTileElems)), which no other wave
+  // touches from here on: no barrier before the store.
+  static_assert(2 * 32 * 64 + 256 <= kTileElems, "staging fits the wave's store tile");
+  __bf16* qs = smem + wave * kTileElems;
+  __bf16* dos = qs + 32 * 64;
+  float* scal = reinterpret_cast<float*>(dos + 32 * 64);  // [0, 32): -L / scale, [64, 96): Delta
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int off = l32 * 64 + (((2 * c + g) ^ swz(l32)) << 3);
+    *reinterpret_cast<bf16x8*>(&qs[off]) = qreg[c];
+    *reinterpret_cast<bf16x8*>(&dos[off]) = doreg[c];
+  }
+  if (g == 0) {
+    scal[l32] = -lse_row / a.scale;
+    scal[64 + l32] = drow;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+
+  const RowIntervals civ = train_col_intervals(key, a.n, a.bs);
+  const ClassBounds cb = uniform_bounds(key_group_bounds(train_key_group(qrow0, 32, a.n, a.bs), a.n));
+  const int cls = bounds_class(cb, qrow0, 32, a.n);
+  f32x16 dk[2] = {}, dv[2] = {};
+  if (cls != kNone) {
+    // S - L / scale and Delta - dP (rows x keys, lane = key), seeded from the row scalars.
+    f32x16 s, dp;
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) {
+      const f32x4 dr = *reinterpret_cast<const f32x4*>(&scal[64 + 8 * rg + 4 * g]);
+      const f32x4 lr = *reinterpret_cast<const f32x4*>(&scal[8 * rg + 4 * g]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        dp[4 * rg + j] = dr[j];
+        s[4 * rg + j] = lr[j];
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      s = mfma32(sw_row_op(qs, 0, c, lane), kreg[c], s);
+      dp = mfma32(sw_row_op(dos, 0, c, lane), vreg[c], dp);
+    }
+    float p[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) p[r] = fast_exp2(s[r] * a.scale_log2);
+    if (cls != kFull) {
+      if (MASK16) {
+        const bool lo = iv_has(civ, qrow0), hi = iv_has(civ, qrow0 + 16);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) p[r] = (r < 8 ? lo : hi) ? p[r] : 0.f;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) p[r] = iv_has(civ, qrow0 + 8 * (r >> 2) + 4 * g + (r & 3)) ? p[r] : 0.f;
+      }
+    }
+    bf16x8 pop[2], dsop[2];  // P^T, -dS^T = (P o (Delta - dP))^T [16-row step]
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc) {
+      pop[kc] = to_bf16x8(p[8 * kc], p[8 * kc + 1], p[8 * kc + 2], p[8 * kc + 3], p[8 * kc + 4], p[8 * kc + 5],
+                          p[8 * kc + 6], p[8 * kc + 7]);
+      dsop[kc] = to_bf16x8(p[8 * kc] * dp[8 * kc], p[8 * kc + 1] * dp[8 * kc + 1], p[8 * kc + 2] * dp[8 * kc + 2],
+                           p[8 * kc + 3] * dp[8 * kc + 3], p[8 * kc + 4] * dp[8 * kc + 4],
+                           p[8 * kc + 5] * dp[8 * kc + 5], p[8 * kc + 6] * dp[8 * kc + 6],
+                           p[8 * kc + 7] * dp[8 * kc + 7]);
+    }
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+      for (int db = 0; db < 2; ++db) {
+        dv[db] = mfma32(pop[kc], sw_tr_op(dos, 16 * kc, 32 * db, lane), dv[db]);
+        dk[db] = mfma32(dsop[kc], sw_tr_op(qs, 16 * kc, 32 * db, lane), dk[db]);
+      }
+  }
+  // The store reuses this wave's tile after its operand reads (in order).
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  dkdv_store(a, smem, b, h, qrow0, wave, lane, dk, dv);
+}
+
 // ---------------------------------------------------------------------------
 // Query-stationary dQ (and Delta). K / V key tiles go global -> LDS with
 // global_load_lds into a three-stage ring of swizzled tiles, two tiles ahead.
@@ -382,9 +497,13 @@ __device__ __forceinline__ void dq_item(const BwdArgs& a, __bf16* smem, int bh, 
   const float drow = a.delta[rowbase + myq];
 
   const KeyRanges kr = train_key_ranges(q0, kBM, a.n, a.bs, kSwRows);
-  const int t0 = wave_uniform(kr.t0), t2 = wave_uniform(kr.t2);
-  const int n_first = wave_uniform(kr.t1 - kr.t0);
-  const int n_tiles = n_first + wave_uniform(kr.t3 - kr.t2);
+  // With the noisy key tiles folded in (odd ranks are noisy row tiles), the
+  // walk takes the clean-key range first and the two diagonal tiles (the
+  // first range) last, so that the epilogue finds their K and V in the ring.
+  const bool fold = a.fold_diag && (rank & 1);
+  const int t0 = wave_uniform(fold ? kr.t2 : kr.t0), t2 = wave_uniform(fold ? kr.t0 : kr.t2);
+  const int n_first = wave_uniform(fold ? kr.t3 - kr.t2 : kr.t1 - kr.t0);
+  const int n_tiles = wave_uniform(kr.t1 - kr.t0 + kr.t3 - kr.t2);
   auto tile_of = [&](int i) { return i < n_first ? t0 + i : t2 + (i - n_first); };
 
   // Wave w fills 1 KB blocks 2w, 2w+1 (rows 16w .. 16w+15) of the K and V tiles.
@@ -508,6 +627,12 @@ __device__ __forceinline__ void dq_item(const BwdArgs& a, __bf16* smem, int bh, 
       *reinterpret_cast<bf16x4*>(dqp + 32 * db + 8 * rg + 4 * g) =
           to_bf16x4(dq[db][4 * rg] * a.scale, dq[db][4 * rg + 1] * a.scale, dq[db][4 * rg + 2] * a.scale,
                     dq[db][4 * rg + 3] * a.scale);
+  // The loop's last barrier left the ring idle, holding the last two tiles:
+  // the diagonal ones (waves 0, 1: the first; waves 2, 3: the second).
+  if (fold) {
+    const int sd = (n_tiles - 2 + (wave >> 1)) % kStages;
+    diag_dkdv<MASK16>(a, smem, bo.b, bo.h, qrow0, wave, lane, stage_k(sd), stage_v(sd), qreg, doreg, lse_row, drow);
+  }
 }
 
 // Delta = rowsum(dO o O) (the reference's separate torch op,

@@ -49,6 +49,10 @@ struct BwdArgs {
   uint16_t order[256];
   int n_items;
   int first_code;
+  // 1: the noisy key tiles' dK/dV (block sizes dividing 32, so only their
+  // diagonal blocks are live) are formed at the end of the dQ items of the
+  // same rows, and the launch holds no dK/dV item for them.
+  int fold_diag;
   Strides3 sq, sk, sv, so, sdo, sdq, sdk, sdv;
   int heads;
   int bh;

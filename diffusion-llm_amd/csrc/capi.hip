@@ -137,8 +137,12 @@ bd3::BwdArgs bwd_args(const void* q, const void* k, const void* v, const void* o
 // query tile c, otherwise dK/dV key tile c - 2n/128.
 void bwd_order(bd3::BwdArgs& a, bool dq, bool dkdv) {
   const int r = 2 * a.n / 128;
+  // With both kinds in the launch and a block size dividing 32, the noisy
+  // key tiles' diagonal blocks are formed by the dQ items of the same rows
+  // (see attn_bwd.hip), so the dK/dV items are the clean key tiles only.
+  a.fold_diag = dq && dkdv && 32 % a.bs == 0;
   a.first_code = dq ? 0 : r;
-  a.n_items = (dq ? r : 0) + (dkdv ? r : 0);
+  a.n_items = (dq ? r : 0) + (dkdv ? (a.fold_diag ? r / 2 : r) : 0);
   if (a.n_items > bd3::kBwdOrderMax) return;  // the kernel walks the codes in order
   int cost[2 * bd3::kBwdOrderMax], codes[bd3::kBwdOrderMax];
   for (int i = 0; i < a.n_items; ++i) {
@@ -147,7 +151,7 @@ void bwd_order(bd3::BwdArgs& a, bool dq, bool dkdv) {
     if (c < r) {
       const int q0 = ((c & 1) ? 0 : a.n) + (r / 2 - 1 - (c >> 1)) * 128;
       const bd3::KeyRanges kr = bd3::train_key_ranges(q0, 128, a.n, a.bs, 64);
-      cost[c] = 3 * ((kr.t1 - kr.t0) + (kr.t3 - kr.t2));
+      cost[c] = 3 * ((kr.t1 - kr.t0) + (kr.t3 - kr.t2)) + (a.fold_diag && (c & 1) ? 3 : 0);
     } else {
       const int kt = c - r;
       const int k0 = kt < r / 2 ? a.n + kt * 128 : (kt - r / 2) * 128;

@@ -124,7 +124,9 @@ int bd3_attn_bwd_delta(const void* o, const void* dout, const float* lse,
  * Backward, main launch: dQ = scale * dS K, dV = P^T dO and dK = scale *
  * dS^T Q from the planes bd3_attn_bwd_delta wrote to `delta`; `lse` is
  * checked but not read (the kernel uses the plane). One launch holds every
- * query-stationary dQ item and key-stationary dK/dV item, longest first.
+ * query-stationary dQ item and key-stationary dK/dV item, longest first;
+ * with a block size dividing 32 the noisy key tiles' dK and dV (their
+ * diagonal blocks) come from the dQ items of the same rows.
  * strides: 21 int64 = (b, h, s) element strides of q, k, v, dout, dq, dk, dv.
  * Preconditions: as bd3_attn_bwd.
  *

@@ -115,9 +115,14 @@ def test_dq_kernel_applies_mask_exactly(cuda, n, bs):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("entry", ["dkdv_stage", "main_launch"])
 @pytest.mark.parametrize("n,bs", [c for c in TRAIN if c[0] % c[1] == 0])
-def test_dkdv_kernel_applies_transposed_mask_exactly(cuda, n, bs):
-    print(f"dK/dV mask n={n} bs={bs}", flush=True)
+def test_dkdv_kernel_applies_transposed_mask_exactly(cuda, n, bs, entry):
+    """dK / dV through the dK/dV stage (bd3_attn_bwd_dkdv: a dK/dV item per
+    key tile) and through the main launch (bd3_attn_bwd_main: with a block
+    size dividing 32 the noisy key tiles' diagonal blocks come from the dQ
+    items of the same rows)."""
+    print(f"dK/dV mask n={n} bs={bs} via {entry}", flush=True)
     H, S = 2, 2 * n
     mask = block_diff_mask(n, bs)
     zeros = dev(np.zeros((S, D), np.float32), H, cuda)
@@ -129,9 +134,15 @@ def test_dkdv_kernel_applies_transposed_mask_exactly(cuda, n, bs):
         q = dev(onehot_rows(S, gmap), H, cuda)
         dout = dev(onehot_rows(S, hmap), H, cuda)
         dk, dv = torch.empty_like(zeros), torch.empty_like(zeros)
-        check(lib().bd3_attn_bwd_dkdv(ptr(q), ptr(zeros), ptr(ones), ptr(dout), ptr(lse), ptr(planes), ptr(dk),
-                                      ptr(dv), 1, H, n, D, bs, strides(q, zeros, ones, dout, dk, dv), SCALE,
-                                      stream_of(q)))
+        if entry == "dkdv_stage":
+            check(lib().bd3_attn_bwd_dkdv(ptr(q), ptr(zeros), ptr(ones), ptr(dout), ptr(lse), ptr(planes), ptr(dk),
+                                          ptr(dv), 1, H, n, D, bs, strides(q, zeros, ones, dout, dk, dv), SCALE,
+                                          stream_of(q)))
+        else:
+            dq = torch.empty_like(zeros)
+            check(lib().bd3_attn_bwd_main(ptr(q), ptr(zeros), ptr(ones), ptr(dout), ptr(lse), ptr(planes), ptr(dq),
+                                          ptr(dk), ptr(dv), 1, H, n, D, bs,
+                                          strides(q, zeros, ones, dout, dq, dk, dv), SCALE, stream_of(q)))
         torch.cuda.synchronize()
         # key j's column: rows i that see j, per bucket of i
         want_k = histogram(mask.T, gmap).astype(np.float64)
