@@ -32,9 +32,11 @@
 //   the noisy rows of its own block, so only the tile's diagonal 32 x 32
 //   blocks are live): in a launch with both kinds they get no dK/dV item;
 //   the dQ item of the same 128 rows walks its two diagonal key tiles last
-//   and, from their K / V still in the ring and its own Q / dO rows, forms
-//   those keys' dK and dV (diag_dkdv). Alone (the dK/dV stage), each such
-//   tile is an item whose waves compute only their diagonal block.
+//   and stops its loop before them: from their K / V still in the ring and
+//   its own Q / dO rows each wave forms its diagonal block once and takes
+//   its rows' dQ and those keys' dK and dV from it (diag_block). Alone (the
+//   dK/dV stage), each such tile is an item whose waves compute only their
+//   diagonal block.
 // Every score is the exact fp32 dot product of the bf16 rows; scale and
 // log2(e) are applied in fp32 (dQ: one FMA per element; dK/dV: the chain
 // starts from -L / scale and the result is multiplied by scale * log2(e)).
@@ -76,11 +78,10 @@ constexpr int kBwdLdsBytes = kDkdvLdsBytes > kDqLdsBytes ? kDkdvLdsBytes : kDqLd
 // dK/dV epilogue (every wave is past its last barrier, no load in flight):
 // each wave transposes its 32 keys x 64 d of dK, then dV, through its own
 // padded LDS slice into row-major bf16, then writes 16-byte row chunks.
-__device__ __forceinline__ void dkdv_store(const BwdArgs& a, __bf16* smem, int b, int h, int kw, int wave, int lane,
+__device__ __forceinline__ void dkdv_store(const BwdArgs& a, __bf16* tile, int b, int h, int kw, int lane,
                                            const f32x16 (&dk)[2], const f32x16 (&dv)[2]) {
   const int l32 = lane & 31;
   const int g = lane >> 5;
-  __bf16* tile = &smem[0] + wave * kTileElems;
   uint16_t* outs[2] = {a.dk + b * a.sdk.b + h * a.sdk.h, a.dv + b * a.sdv.b + h * a.sdv.h};
   const int64_t ostr[2] = {a.sdk.s, a.sdv.s};
 #pragma unroll
@@ -294,7 +295,7 @@ __device__ __forceinline__ void dkdv_item(const BwdArgs& a, __bf16* smem, int bh
         }
     }
     vm_wait_barrier<0>();
-    dkdv_store(a, smem, bo.b, bo.h, kw, wave, lane, dk, dv);
+    dkdv_store(a, smem + wave * kTileElems, bo.b, bo.h, kw, lane, dk, dv);
     return;
   }
   int cur = 0;
@@ -333,45 +334,55 @@ __device__ __forceinline__ void dkdv_item(const BwdArgs& a, __bf16* smem, int bh
     cur = cur == 2 ? 0 : cur + 1;
   }
 
-  dkdv_store(a, smem, bo.b, bo.h, kw, wave, lane, dk, dv);
+  dkdv_store(a, smem + wave * kTileElems, bo.b, bo.h, kw, lane, dk, dv);
 }
 
-// The dK and dV of the noisy keys with the same indices as a dQ item's wave's
-// 32 noisy rows (fold_diag: block sizes dividing 32). Such a key is seen only
-// by the noisy rows of its own block, all of them this wave's, so the wave's
-// 32 x 32 diagonal block gives the keys' whole dK and dV: the DIAG path of
-// dkdv_item on that one block. The dQ item walks its diagonal key tiles last,
-// so their K and V are still in the ring; the wave's Q and dO rows (held in
-// registers by the dQ item) are then staged into a wave-private swizzled
-// tile for the transposed operand reads. Every wave writes its own 32 keys
-// through its own LDS tile.
+// The diagonal 32 x 32 block of a dQ item's wave when the noisy key tiles
+// are folded in (fold_diag: block sizes dividing 32). A noisy key is seen
+// only by the noisy rows of its own block, all of them in the wave whose
+// rows have the key's indices, so this one block gives those 32 keys' whole
+// dK and dV and the wave's rows' dQ over their own block: S and dP are formed
+// once for dQ, dK and dV (the dQ loop stops before the two diagonal key
+// tiles, which it walks last, so their K and V are still in the ring).
+// dK/dV take the dK/dV items' arithmetic and layouts (key per lane): S = Q K^T
+// and Delta - dP from the wave's own Q / dO operand registers, P and -dS,
+// dV += P^T dO, dK += (-dS)^T Q with dO / Q read transposed from a staging
+// tile. dQ^T += K^T dS^T takes dS^T through the staging as well (written key
+// by row, read transposed, so its key order matches K^T's). Each wave then
+// stores its own keys' rows through its own staging region.
 template <bool MASK16>
-__device__ __forceinline__ void diag_dkdv(const BwdArgs& a, __bf16* smem, int b, int h, int qrow0, int wave, int lane,
-                                          const __bf16* ktile, const __bf16* vtile, const bf16x8 (&qreg)[4],
-                                          const bf16x8 (&doreg)[4], float lse_row, float drow) {
+__device__ __forceinline__ void diag_block(const BwdArgs& a, __bf16* smem, int b, int h, int qrow0, int wave, int lane,
+                                           const __bf16* ktile, const __bf16* vtile, const bf16x8 (&qreg)[4],
+                                           const bf16x8 (&doreg)[4], float lse_row, float drow, f32x16 (&dq)[2]) {
+  constexpr int kRegion = 3 * 32 * 64 + 256;  // bf16: Q rows, dO rows, dS^T, 128 row scalars
+  static_assert(4 * kRegion * 2 <= kBwdLdsBytes, "four staging regions fit the LDS buffer");
+  static_assert(32 * kLdsStride <= kRegion, "the store's 32 rows fit a region");
   const int l32 = lane & 31;
   const int g = lane >> 5;
   const int key = qrow0 + l32;
-  // K rows and negated V rows of the wave's 32 keys: rows 32 (wave % 2) of
-  // the ring's K and V tiles of the diagonal tile, which the dQ loop visited
-  // last. Every wave holds them before the ring is reused for the staging.
-  bf16x8 kreg[4], vreg[4];
+  const int kr0 = 32 * (wave & 1);  // the wave's keys: rows kr0 .. kr0 + 31 of its diagonal tile
+  // From the ring, before any wave reuses it: K rows and negated V rows (B
+  // operands of S and dP) and K^T (A operands of dQ^T += K^T dS^T).
+  bf16x8 kreg[4], vreg[4], kt[2][2];
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
-    kreg[c] = sw_row_op(ktile, 32 * (wave & 1), c, lane);
-    vreg[c] = __builtin_bit_cast(bf16x8, __builtin_bit_cast(u32x4, sw_row_op(vtile, 32 * (wave & 1), c, lane)) ^
-                                             0x80008000u);
+    kreg[c] = sw_row_op(ktile, kr0, c, lane);
+    vreg[c] = __builtin_bit_cast(bf16x8, __builtin_bit_cast(u32x4, sw_row_op(vtile, kr0, c, lane)) ^ 0x80008000u);
   }
 #pragma unroll
+  for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+    for (int db = 0; db < 2; ++db) kt[kc][db] = sw_tr_op(ktile, kr0 + 16 * kc, 32 * db, lane);
+#pragma unroll
   for (int c = 0; c < 4; ++c) asm volatile("" ::"v"(kreg[c]), "v"(vreg[c]));
+#pragma unroll
+  for (int kc = 0; kc < 2; ++kc) asm volatile("" ::"v"(kt[kc][0]), "v"(kt[kc][1]));
   __syncthreads();
-  // The wave's staging lies inside the LDS tile its dkdv_store uses (wave w:
-  // elements [w kTileElems, (w + 1) kTileElems)), which no other wave
-  // touches from here on: no barrier before the store.
-  static_assert(2 * 32 * 64 + 256 <= kTileElems, "staging fits the wave's store tile");
-  __bf16* qs = smem + wave * kTileElems;
+
+  __bf16* qs = smem + wave * kRegion;
   __bf16* dos = qs + 32 * 64;
-  float* scal = reinterpret_cast<float*>(dos + 32 * 64);  // [0, 32): -L / scale, [64, 96): Delta
+  __bf16* dst = dos + 32 * 64;                           // dS^T: row = key, column = query row
+  float* scal = reinterpret_cast<float*>(dst + 32 * 64);  // [0, 32): -L / scale, [64, 96): Delta
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     const int off = l32 * 64 + (((2 * c + g) ^ swz(l32)) << 3);
@@ -404,8 +415,8 @@ __device__ __forceinline__ void diag_dkdv(const BwdArgs& a, __bf16* smem, int b,
     }
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      s = mfma32(sw_row_op(qs, 0, c, lane), kreg[c], s);
-      dp = mfma32(sw_row_op(dos, 0, c, lane), vreg[c], dp);
+      s = mfma32(qreg[c], kreg[c], s);
+      dp = mfma32(doreg[c], vreg[c], dp);
     }
     float p[16];
 #pragma unroll
@@ -429,6 +440,12 @@ __device__ __forceinline__ void diag_dkdv(const BwdArgs& a, __bf16* smem, int b,
                            p[8 * kc + 3] * dp[8 * kc + 3], p[8 * kc + 4] * dp[8 * kc + 4],
                            p[8 * kc + 5] * dp[8 * kc + 5], p[8 * kc + 6] * dp[8 * kc + 6],
                            p[8 * kc + 7] * dp[8 * kc + 7]);
+      // dS^T row `key`, columns (query rows) 16kc + 4g .. +3 and 16kc + 8 + 4g .. +3:
+      // +dS (the sign bit flipped, exact), 8 bytes each.
+      const u32x4 ds4 = __builtin_bit_cast(u32x4, dsop[kc]) ^ 0x80008000u;
+      const int c0 = 16 * kc + 4 * g, c1 = c0 + 8;
+      *reinterpret_cast<u32x2*>(&dst[l32 * 64 + (((c0 >> 3) ^ swz(l32)) << 3) + (c0 & 7)]) = u32x2{ds4[0], ds4[1]};
+      *reinterpret_cast<u32x2*>(&dst[l32 * 64 + (((c1 >> 3) ^ swz(l32)) << 3) + (c1 & 7)]) = u32x2{ds4[2], ds4[3]};
     }
 #pragma unroll
     for (int kc = 0; kc < 2; ++kc)
@@ -437,11 +454,17 @@ __device__ __forceinline__ void diag_dkdv(const BwdArgs& a, __bf16* smem, int b,
         dv[db] = mfma32(pop[kc], sw_tr_op(dos, 16 * kc, 32 * db, lane), dv[db]);
         dk[db] = mfma32(dsop[kc], sw_tr_op(qs, 16 * kc, 32 * db, lane), dk[db]);
       }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+      for (int db = 0; db < 2; ++db) dq[db] = mfma32(kt[kc][db], sw_tr_op(dst, 16 * kc, 0, lane), dq[db]);
   }
-  // The store reuses this wave's tile after its operand reads (in order).
+  // The store reuses this wave's region after its operand reads (in order).
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
-  dkdv_store(a, smem, b, h, qrow0, wave, lane, dk, dv);
+  dkdv_store(a, qs, b, h, qrow0, lane, dk, dv);
 }
 
 // ---------------------------------------------------------------------------
@@ -587,10 +610,13 @@ __device__ __forceinline__ void dq_item(const BwdArgs& a, __bf16* smem, int bh, 
                            ds[8 * kc + 5], ds[8 * kc + 6], ds[8 * kc + 7]);
   };
 
-  // Every row group sees at least its own block, so n_tiles >= 1.
+  // Every row group sees at least its own block, so n_tiles >= 1. Folded:
+  // the two diagonal tiles (the walk's last) are left to diag_block; a noisy
+  // row tile also sees clean keys, so the loop keeps at least one tile.
   vm_wait_barrier<0>();
+  const int n_loop = fold ? n_tiles - 2 : n_tiles;
   int cur = 0;
-  for (int it = 0; it < n_tiles; ++it) {
+  for (int it = 0; it < n_loop; ++it) {
     const bool pf = it + kAhead < n_tiles;
     if (pf) issue(cur + kAhead < kStages ? cur + kAhead : cur + kAhead - kStages);
     const int k0 = wave_uniform(tile_of(it) * kSwRows);
@@ -619,6 +645,15 @@ __device__ __forceinline__ void dq_item(const BwdArgs& a, __bf16* smem, int bh, 
     cur = cur + 1 == kStages ? 0 : cur + 1;
   }
 
+  if (fold) {
+    // Both diagonal tiles resident (the loop's last wait left the second in
+    // flight) and no wave still in the loop: waves 0, 1 take their keys from
+    // the first diagonal tile, waves 2, 3 from the second.
+    vm_wait_barrier<0>();
+    const int sd = (n_tiles - 2 + (wave >> 1)) % kStages;
+    diag_block<MASK16>(a, smem, bo.b, bo.h, qrow0, wave, lane, stage_k(sd), stage_v(sd), qreg, doreg, lse_row, drow,
+                       dq);
+  }
   uint16_t* dqp = a.dq + bo.b * a.sdq.b + bo.h * a.sdq.h + (int64_t)myq * a.sdq.s;
 #pragma unroll
   for (int db = 0; db < 2; ++db)
@@ -627,12 +662,6 @@ __device__ __forceinline__ void dq_item(const BwdArgs& a, __bf16* smem, int bh, 
       *reinterpret_cast<bf16x4*>(dqp + 32 * db + 8 * rg + 4 * g) =
           to_bf16x4(dq[db][4 * rg] * a.scale, dq[db][4 * rg + 1] * a.scale, dq[db][4 * rg + 2] * a.scale,
                     dq[db][4 * rg + 3] * a.scale);
-  // The loop's last barrier left the ring idle, holding the last two tiles:
-  // the diagonal ones (waves 0, 1: the first; waves 2, 3: the second).
-  if (fold) {
-    const int sd = (n_tiles - 2 + (wave >> 1)) % kStages;
-    diag_dkdv<MASK16>(a, smem, bo.b, bo.h, qrow0, wave, lane, stage_k(sd), stage_v(sd), qreg, doreg, lse_row, drow);
-  }
 }
 
 // Delta = rowsum(dO o O) (the reference's separate torch op,

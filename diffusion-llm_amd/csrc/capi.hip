@@ -904,6 +904,11 @@ int bd3_train_tile_census(int32_t n, int32_t block_size, int64_t* out) {
             exec_keys += 32 * 64;
         }
   }
+  // The main launch's dQ items: the forward's schedule, except that with a
+  // block size dividing 32 each noisy 32-row wave forms only its diagonal
+  // 32 x 32 block of its one live diagonal key tile (a 32 x 64 tile in the
+  // forward's count).
+  const int64_t exec_dq = 32 % block_size == 0 ? exec_rows - (int64_t)(n / 32) * (32 * 64 - 32 * 32) : exec_rows;
   const int64_t nn = n, bs = block_size;
   out[0] = useful;
   out[1] = exec_rows;
@@ -911,7 +916,7 @@ int bd3_train_tile_census(int32_t n, int32_t block_size, int64_t* out) {
   out[3] = partial;
   out[4] = skipped;
   out[5] = nn * nn + nn * bs;
-  out[6] = exec_rows;
+  out[6] = exec_dq;
   out[7] = exec_keys;
   return BD3_OK;
 }
