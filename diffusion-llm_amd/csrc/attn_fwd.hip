@@ -9,6 +9,9 @@
 // 32 rows; a query tile lies in one half. Only key tiles (64 keys) where the
 // mask has live pairs for the workgroup are visited (train_key_ranges); each
 // wave skips tiles that are dead for its rows and masks only partial ones.
+// Noisy rows with a block size dividing 32 start with their own two noisy
+// key tiles loaded at once: each wave forms only its 32 x 32 diagonal block,
+// all four waves in one half-tile step.
 //
 // Loads: K/V tiles go global -> LDS with global_load_lds_dwordx4 into a
 // ring of swizzled tiles (bd3_swz.h): no VGPR staging and no LDS store pass;
@@ -181,9 +184,22 @@ __device__ __forceinline__ void fwd_body(Args a) {
   // latencies overlap. Consuming Q here (an empty asm reading it) makes the
   // compiler place its own wait for the Q loads at this point; that wait
   // also covers the direct loads issued after them, which is harmless.
+  // Noisy rows with a block size dividing 32 (training, two-stage ring): the
+  // walk's first two tiles are the workgroup's own noisy blocks, where each
+  // wave's live pairs form the 32 x 32 block of its own rows (keys qrow0 ..
+  // qrow0 + 31). Both tiles are loaded at once and every wave forms its block
+  // in one half-tile step, instead of a whole-tile step on one of the two
+  // tiles while the other two waves wait at its barrier.
+  bool diag_first = false;
+  if constexpr (!PREFILL && kStages == 2) diag_first = q0 < a.n && 32 % a.bs == 0;
+  if (diag_first) {
+    issue(0);
+    issue(1);
+  } else {
 #pragma unroll
-  for (int i = 0; i < kAhead; ++i)
-    if (i < n_tiles) issue(i);
+    for (int i = 0; i < kAhead; ++i)
+      if (i < n_tiles) issue(i);
+  }
 #pragma unroll
   for (int c = 0; c < 4; ++c) asm volatile("" ::"v"(qreg[c]));
   RowIntervals riv;
@@ -221,13 +237,38 @@ __device__ __forceinline__ void fwd_body(Args a) {
 
   // One tile step over NSB 32-key halves of the current 64-key tile,
   // starting at half sb0 (NSB = 1: the other half is dead for this wave).
-  auto step = [&](auto nsb_c, int sb0, int k0, int cls, const __bf16* ks, const __bf16* vs) {
+  // EARLY: the V^T operands are read together with the K operands, and once
+  // both are in registers `reads_done` runs (the tile's LDS may then be
+  // refilled while the step computes).
+  auto step = [&](auto nsb_c, auto early_c, int sb0, int k0, int cls, const __bf16* ks, const __bf16* vs,
+                  auto&& reads_done) {
     constexpr int NSB = decltype(nsb_c)::value;
+    constexpr bool EARLY = decltype(early_c)::value;
     bf16x8 kop[NSB][4];
 #pragma unroll
     for (int sb = 0; sb < NSB; ++sb)
 #pragma unroll
       for (int c = 0; c < 4; ++c) kop[sb][c] = sw_row_op(ks, 32 * (sb0 + sb), c, lane);
+    bf16x8 vpre[EARLY ? NSB : 1][2][2];
+    if constexpr (EARLY) {
+#pragma unroll
+      for (int sb = 0; sb < NSB; ++sb)
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+          for (int db = 0; db < 2; ++db) vpre[sb][kc][db] = sw_tr_op(vs, 32 * (sb0 + sb) + 16 * kc, 32 * db, lane);
+#pragma unroll
+      for (int sb = 0; sb < NSB; ++sb)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) asm volatile("" ::"v"(kop[sb][c]));
+#pragma unroll
+      for (int sb = 0; sb < NSB; ++sb)
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+          for (int db = 0; db < 2; ++db) asm volatile("" ::"v"(vpre[sb][kc][db]));
+      reads_done();
+    }
     f32x16 s[NSB];
 #pragma unroll
     for (int sb = 0; sb < NSB; ++sb) s[sb] = mfma32(kop[sb][0], qreg[0], f32x16{});
@@ -304,7 +345,12 @@ __device__ __forceinline__ void fwd_body(Args a) {
 #pragma unroll
       for (int kc = 0; kc < 2; ++kc)
 #pragma unroll
-        for (int db = 0; db < 2; ++db) vop[kc][db] = sw_tr_op(vs, 32 * (sb0 + sb) + 16 * kc, 32 * db, lane);
+        for (int db = 0; db < 2; ++db) {
+          if constexpr (EARLY)
+            vop[kc][db] = vpre[sb][kc][db];
+          else
+            vop[kc][db] = sw_tr_op(vs, 32 * (sb0 + sb) + 16 * kc, 32 * db, lane);
+        }
 #pragma unroll
       for (int kc = 0; kc < 2; ++kc)
 #pragma unroll
@@ -315,15 +361,28 @@ __device__ __forceinline__ void fwd_body(Args a) {
   // Every row group sees at least its own block, so n_tiles >= 1.
   vm_wait_barrier<0>();
 
-  int cur = 0;
-  for (int it = 0; it < n_tiles; ++it) {
+  int it = 0, cur = 0;
+  if (diag_first) {
+    // Wave w's block lies in half w % 2 of tile w / 2 (stage w / 2). Once
+    // every wave holds its operands, stage 0 takes the first tile of the
+    // loop, which loads while the blocks are formed.
+    const int st = wave >> 1;
+    step(std::integral_constant<int, 1>(), std::true_type(), wave & 1, wave_uniform(tile_of(st) * kSwRows),
+         a.bs == 32 ? kFull : kPartial, smem[st][0], smem[st][1], [&] {
+           vm_wait_barrier<0>();
+           if (n_tiles > 2) issue(0);
+         });
+    it = 2;
+    vm_wait_barrier<0>();
+  }
+  for (; it < n_tiles; ++it) {
     const bool pf = it + kAhead < n_tiles;
     if (pf) issue(cur + kAhead < kStages ? cur + kAhead : cur + kAhead - kStages);
     const int k0 = wave_uniform(tile_of(it) * kSwRows);
     // The tile's class for this wave's rows.
     if (walk_live(wc, it, n_first))
-      step(std::integral_constant<int, 2>(), 0, k0, walk_full(wc, it, n_first) ? kFull : kPartial, smem[cur][0],
-           smem[cur][1]);
+      step(std::integral_constant<int, 2>(), std::false_type(), 0, k0,
+           walk_full(wc, it, n_first) ? kFull : kPartial, smem[cur][0], smem[cur][1], [] {});
     // Tile it+1 complete (the loads of later tiles may stay in flight), and
     // every wave is done reading stage `cur` before it is refilled.
     if (pf)
