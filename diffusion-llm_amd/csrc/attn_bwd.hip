@@ -239,23 +239,24 @@ __device__ __forceinline__ void dkdv_item(const BwdArgs& a, __bf16* smem, int bh
   // dP). A block that is not fully visible gets P = 0 on its invisible
   // pairs: with MASK16 (block size a multiple of 16) the mask is constant on
   // 16-row x 1-key strips, so one test per lane for rows 0-15 of the block
-  // (registers 0-7) and one for rows 16-31 decide it; otherwise every pair
-  // is tested. A dead block is computed and fully masked.
+  // (registers 0-7) and one for rows 16-31 decide it, and it enters the
+  // exponent as an addend (0, or -inf for an invisible strip: exp2 gives 0);
+  // otherwise every pair is tested. A dead block is computed and fully
+  // masked.
   auto softmax_ops = [&](const f32x16& s, const f32x16& dp, int q0, int qb, bool masked, bf16x8 (&pop)[2],
                          bf16x8 (&dsop)[2]) {
+    float blo = 0.f, bhi = 0.f;  // exponent addends of registers 0-7 and 8-15
+    if (MASK16 && masked) {
+      blo = iv_has(civ, q0 + 32 * qb) ? 0.f : -INFINITY;
+      bhi = iv_has(civ, q0 + 32 * qb + 16) ? 0.f : -INFINITY;
+    }
     float p[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) p[r] = fast_exp2(s[r] * a.scale_log2);
-    if (masked) {
-      if (MASK16) {
-        const bool lo = iv_has(civ, q0 + 32 * qb), hi = iv_has(civ, q0 + 32 * qb + 16);
+    for (int r = 0; r < 16; ++r) p[r] = fast_exp2(fmaf(s[r], a.scale_log2, r < 8 ? blo : bhi));
+    if (!MASK16 && masked) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) p[r] = (r < 8 ? lo : hi) ? p[r] : 0.f;
-      } else {
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          p[r] = iv_has(civ, q0 + 32 * qb + 8 * (r >> 2) + 4 * g + (r & 3)) ? p[r] : 0.f;
-      }
+      for (int r = 0; r < 16; ++r)
+        p[r] = iv_has(civ, q0 + 32 * qb + 8 * (r >> 2) + 4 * g + (r & 3)) ? p[r] : 0.f;
     }
     float ds[16];  // -dS
 #pragma unroll
@@ -418,18 +419,18 @@ __device__ __forceinline__ void diag_block(const BwdArgs& a, __bf16* smem, int b
       s = mfma32(qreg[c], kreg[c], s);
       dp = mfma32(doreg[c], vreg[c], dp);
     }
+    // Mask as in the dK/dV items: MASK16 strips through the exponent's addend.
+    float blo = 0.f, bhi = 0.f;
+    if (MASK16 && cls != kFull) {
+      blo = iv_has(civ, qrow0) ? 0.f : -INFINITY;
+      bhi = iv_has(civ, qrow0 + 16) ? 0.f : -INFINITY;
+    }
     float p[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) p[r] = fast_exp2(s[r] * a.scale_log2);
-    if (cls != kFull) {
-      if (MASK16) {
-        const bool lo = iv_has(civ, qrow0), hi = iv_has(civ, qrow0 + 16);
+    for (int r = 0; r < 16; ++r) p[r] = fast_exp2(fmaf(s[r], a.scale_log2, r < 8 ? blo : bhi));
+    if (!MASK16 && cls != kFull) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) p[r] = (r < 8 ? lo : hi) ? p[r] : 0.f;
-      } else {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) p[r] = iv_has(civ, qrow0 + 8 * (r >> 2) + 4 * g + (r & 3)) ? p[r] : 0.f;
-      }
+      for (int r = 0; r < 16; ++r) p[r] = iv_has(civ, qrow0 + 8 * (r >> 2) + 4 * g + (r & 3)) ? p[r] : 0.f;
     }
     bf16x8 pop[2], dsop[2];  // P^T, -dS^T = (P o (Delta - dP))^T [16-row step]
 #pragma unroll
@@ -572,8 +573,10 @@ __device__ __forceinline__ void dq_item(const BwdArgs& a, __bf16* smem, int bh, 
   // r%4), P, dS. A block that is not fully visible gets P = 0 on its
   // invisible pairs: with MASK16 (block size a multiple of 16) the mask is
   // constant on 1-row x 16-key strips, so one test per lane for keys 0-15 of
-  // the block (registers 0-7) and one for keys 16-31 decide it; otherwise
-  // every pair is tested. A dead block is computed and fully masked.
+  // the block (registers 0-7) and one for keys 16-31 decide it, and it
+  // enters the exponent as its addend (-L, or -inf for an invisible strip);
+  // otherwise every pair is tested. A dead block is computed and fully
+  // masked.
   auto block_ops = [&](const __bf16* ks, const __bf16* vs, int k0, int sb, bool masked, bf16x8 (&dsop)[2]) {
     bf16x8 kop[4], vop[4];
 #pragma unroll
@@ -587,19 +590,18 @@ __device__ __forceinline__ void dq_item(const BwdArgs& a, __bf16* smem, int bh, 
       s = mfma32(kop[c], qreg[c], s);
       dp = mfma32(vop[c], doreg[c], dp);
     }
+    float blo = -lrow, bhi = -lrow;  // exponent addends of registers 0-7 and 8-15
+    if (MASK16 && masked) {
+      blo = iv_has(riv, k0 + 32 * sb) ? -lrow : -INFINITY;
+      bhi = iv_has(riv, k0 + 32 * sb + 16) ? -lrow : -INFINITY;
+    }
     float p[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) p[r] = fast_exp2(fmaf(s[r], a.scale_log2, -lrow));
-    if (masked) {
-      if (MASK16) {
-        const bool lo = iv_has(riv, k0 + 32 * sb), hi = iv_has(riv, k0 + 32 * sb + 16);
+    for (int r = 0; r < 16; ++r) p[r] = fast_exp2(fmaf(s[r], a.scale_log2, r < 8 ? blo : bhi));
+    if (!MASK16 && masked) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) p[r] = (r < 8 ? lo : hi) ? p[r] : 0.f;
-      } else {
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          p[r] = iv_has(riv, k0 + 32 * sb + 8 * (r >> 2) + 4 * g + (r & 3)) ? p[r] : 0.f;
-      }
+      for (int r = 0; r < 16; ++r)
+        p[r] = iv_has(riv, k0 + 32 * sb + 8 * (r >> 2) + 4 * g + (r & 3)) ? p[r] : 0.f;
     }
     float ds[16];
 #pragma unroll
