@@ -277,18 +277,20 @@ __device__ __forceinline__ void fwd_body(Args a) {
 #pragma unroll
       for (int sb = 0; sb < NSB; ++sb) s[sb] = mfma32(kop[sb][c], qreg[c], s[sb]);
 
-    // Partial tile: invisible pairs to -inf. With MASK16 (block size a
-    // multiple of 16) the mask is constant on 1-row x 16-key strips:
-    // registers 0-7 of a key block hold its keys 0-15, registers 8-15 keys
-    // 16-31, so one test per strip decides them.
+    // Partial tile. With MASK16 (block size a multiple of 16) the mask is
+    // constant on 1-row x 16-key strips: registers 0-7 of a key block hold
+    // its keys 0-15, registers 8-15 keys 16-31, so one test per strip decides
+    // them; an invisible strip is left out of the row max and enters the
+    // exponent with a -inf addend (P = 0). Otherwise invisible pairs are set
+    // to -inf one by one.
+    bool live[NSB][2];  // MASK16 partial tile: strip h of key block sb visible to the lane's row
     if (cls == kPartial) {
 #pragma unroll
       for (int sb = 0; sb < NSB; ++sb) {
         const int kb = k0 + 32 * (sb0 + sb);
         if (MASK16) {
-          const bool lo = iv_has(riv, kb), hi = iv_has(riv, kb + 16);
-#pragma unroll
-          for (int r = 0; r < 16; ++r) s[sb][r] = (r < 8 ? lo : hi) ? s[sb][r] : -INFINITY;
+          live[sb][0] = iv_has(riv, kb);
+          live[sb][1] = iv_has(riv, kb + 16);
         } else {
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
@@ -298,20 +300,29 @@ __device__ __forceinline__ void fwd_body(Args a) {
         }
       }
     }
-    // Row max of the scores: four independent v_max3 chains, then scaled to
-    // the base-2 exponent relative to the current reference.
-    float mq[4];
+    // Row max of the scores: one v_max3 chain per strip, then scaled to the
+    // base-2 exponent relative to the current reference.
+    float mst[NSB][2];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      mq[q] = fmaxf(fmaxf(s[0][4 * q], s[0][4 * q + 1]), s[0][4 * q + 2]);
-      mq[q] = fmaxf(mq[q], s[0][4 * q + 3]);
+    for (int sb = 0; sb < NSB; ++sb)
 #pragma unroll
-      for (int sb = 1; sb < NSB; ++sb) {
-        mq[q] = fmaxf(fmaxf(mq[q], s[sb][4 * q]), s[sb][4 * q + 1]);
-        mq[q] = fmaxf(fmaxf(mq[q], s[sb][4 * q + 2]), s[sb][4 * q + 3]);
+      for (int hh = 0; hh < 2; ++hh) {
+        const int r0 = 8 * hh;
+        float m = fmaxf(fmaxf(s[sb][r0], s[sb][r0 + 1]), s[sb][r0 + 2]);
+        m = fmaxf(fmaxf(m, s[sb][r0 + 3]), s[sb][r0 + 4]);
+        m = fmaxf(fmaxf(m, s[sb][r0 + 5]), s[sb][r0 + 6]);
+        mst[sb][hh] = fmaxf(m, s[sb][r0 + 7]);
       }
+    if (MASK16 && cls == kPartial) {
+#pragma unroll
+      for (int sb = 0; sb < NSB; ++sb)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) mst[sb][hh] = live[sb][hh] ? mst[sb][hh] : -INFINITY;
     }
-    const float mt = fmaf(max_xor32(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]))), c2, -mref);
+    float mrow = fmaxf(mst[0][0], mst[0][1]);
+#pragma unroll
+    for (int sb = 1; sb < NSB; ++sb) mrow = fmaxf(fmaxf(mrow, mst[sb][0]), mst[sb][1]);
+    const float mt = fmaf(max_xor32(mrow), c2, -mref);
     // A new reference when the row had none (and this tile has a live key)
     // or its maximum grew by more than kRescale: the reference rises by
     // delta, O and l scale by 2^-delta.
@@ -324,12 +335,22 @@ __device__ __forceinline__ void fwd_body(Args a) {
       o[0] *= alpha;
       o[1] *= alpha;
     }
+    // Exponent addends per strip: -mref, or -inf for an invisible strip.
+    float nm[NSB][2];
+#pragma unroll
+    for (int sb = 0; sb < NSB; ++sb) nm[sb][0] = nm[sb][1] = -mref;
+    if (MASK16 && cls == kPartial) {
+#pragma unroll
+      for (int sb = 0; sb < NSB; ++sb)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) nm[sb][hh] = live[sb][hh] ? -mref : -INFINITY;
+    }
     bf16x8 pop[NSB][2];  // P^T operands [key block][16-key step]
 #pragma unroll
     for (int sb = 0; sb < NSB; ++sb) {
       float p[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) p[r] = fast_exp2(fmaf(s[sb][r], c2, -mref));
+      for (int r = 0; r < 16; ++r) p[r] = fast_exp2(fmaf(s[sb][r], c2, nm[sb][r >> 3]));
       // The row sum in fp32 from the unrounded P, as the reference's l.
 #pragma unroll
       for (int kc = 0; kc < 2; ++kc) {
