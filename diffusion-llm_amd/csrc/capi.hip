@@ -865,7 +865,8 @@ int bd3_train_tile_census(int32_t n, int32_t block_size, int64_t* out) {
   for (int q = 0; q < 2 * n; ++q) useful += bd3::train_row_keys(q, n, block_size);
   // Query-stationary schedule (forward, dQ items): 128-row workgroups
   // visit the 64-key tiles of train_key_ranges; each 32-row wave computes
-  // both 32-key halves of a tile when either holds a live pair for its rows.
+  // both 32-key halves of a tile when either holds a live pair for its rows
+  // (the noisy diagonal aside, below).
   for (int q0 = 0; q0 < 2 * n; q0 += 128) {
     const bd3::KeyRanges kr = bd3::train_key_ranges(q0, 128, n, block_size, 64);
     const int ranges[2][2] = {{kr.t0, kr.t1}, {kr.t2, kr.t3}};
@@ -904,14 +905,13 @@ int bd3_train_tile_census(int32_t n, int32_t block_size, int64_t* out) {
             exec_keys += 32 * 64;
         }
   }
-  // The main launch's dQ items: the forward's schedule, except that with a
-  // block size dividing 32 each noisy 32-row wave forms only its diagonal
-  // 32 x 32 block of its one live diagonal key tile (a 32 x 64 tile in the
-  // forward's count).
+  // The forward and the main launch's dQ items: with a block size dividing
+  // 32 each noisy 32-row wave forms only its diagonal 32 x 32 block of its
+  // one live diagonal key tile (a whole 32 x 64 tile in the count above).
   const int64_t exec_dq = 32 % block_size == 0 ? exec_rows - (int64_t)(n / 32) * (32 * 64 - 32 * 32) : exec_rows;
   const int64_t nn = n, bs = block_size;
   out[0] = useful;
-  out[1] = exec_rows;
+  out[1] = exec_dq;
   out[2] = full;
   out[3] = partial;
   out[4] = skipped;

@@ -423,12 +423,12 @@ int bd3_clock_probe(uint64_t* out, int32_t workgroups, int32_t iters, int64_t* w
  * schedules for one (batch, head). Writes out[0..7] =
  *   {useful pairs,
  *    pairs the forward kernel computes (its 32-row waves compute both 32-key
- *      halves of a 64-key tile when either half has a live pair),
+ *      halves of a 64-key tile when either half has a live pair; when
+ *      32 % block_size == 0 each noisy 32-row wave computes only its
+ *      diagonal 32 x 32 block of the noisy keys),
  *    full / partial / skipped 32x32 sub-blocks of that schedule,
  *    useful pairs per (b,h) closed form n^2 + n*bs,
- *    pairs the main launch's dQ items compute (the forward's schedule;
- *      when 32 % block_size == 0 each noisy 32-row wave computes only its
- *      diagonal 32 x 32 block of the noisy keys),
+ *    pairs the main launch's dQ items compute (the forward's schedule),
  *    pairs the dK/dV work computes (32-key waves, both 32-row halves of a
  *      64-row tile when either has a live pair; when 32 % block_size == 0
  *      only the diagonal 32 x 32 block of a noisy key tile's waves)}.

@@ -59,15 +59,14 @@ def test_census_matches_oracle(lib, n, bs):
         assert np.array_equal(diag, np.eye(n // 32, dtype=bool))
         keys[:, : n // 32] = False
         assert out[7] == 2048 * int(keys.sum()) + 1024 * (n // 32)
-        # the main launch's dQ items: each noisy 32-row wave's one live noisy 64-key tile
-        # becomes its diagonal 32 x 32 block
+        # the forward and the main launch's dQ items: each noisy 32-row wave's one live
+        # noisy 64-key tile becomes its diagonal 32 x 32 block
         noisy = rows[: n // 32, : n // 64]
         assert np.array_equal(noisy.sum(axis=1), np.ones(n // 32, dtype=int))
-        assert out[6] == 2048 * int(rows.sum()) - 1024 * (n // 32)
+        assert out[6] == out[1] == 2048 * int(rows.sum()) - 1024 * (n // 32)
     else:
         assert out[7] == 2048 * int(keys.sum())
-        assert out[6] == 2048 * int(rows.sum())
-    assert out[1] == 2048 * int(rows.sum())
+        assert out[6] == out[1] == 2048 * int(rows.sum())
     assert out[1] >= 1024 * (out[2] + out[3]) >= out[0]
 
 
