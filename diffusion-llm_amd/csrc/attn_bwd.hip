@@ -314,20 +314,25 @@ __device__ __forceinline__ void dkdv_item(const BwdArgs& a, __bf16* smem, int bh
       const float* scal = reinterpret_cast<const float*>(qs + 2 * kSwTile);
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
-        f32x16 sc, dpc;
-        block_products(qs, dos, scal, qb, sc, dpc);
-        bf16x8 pop[2], dsop[2];  // [16-row step]
-        softmax_ops(sc, dpc, q0, qb, (qb ? c1 : c0) != kFull, pop, dsop);
-        // dV += P^T dO, dK += dS^T Q with dO / Q read transposed.
+        // MASK16: a 32-row block with no live pair is skipped (the first
+        // block of a range's first tile for some waves; the per-pair mask
+        // instance computes it, which keeps its registers).
+        if (!MASK16 || (qb ? c1 : c0) != kNone) {
+          f32x16 sc, dpc;
+          block_products(qs, dos, scal, qb, sc, dpc);
+          bf16x8 pop[2], dsop[2];  // [16-row step]
+          softmax_ops(sc, dpc, q0, qb, (qb ? c1 : c0) != kFull, pop, dsop);
+          // dV += P^T dO, dK += dS^T Q with dO / Q read transposed.
 #pragma unroll
-        for (int kc = 0; kc < 2; ++kc)
+          for (int kc = 0; kc < 2; ++kc)
 #pragma unroll
-          for (int db = 0; db < 2; ++db) {
-            const bf16x8 dot = sw_tr_op(dos, 32 * qb + 16 * kc, 32 * db, lane);
-            const bf16x8 qt = sw_tr_op(qs, 32 * qb + 16 * kc, 32 * db, lane);
-            dv[db] = mfma32(pop[kc], dot, dv[db]);
-            dk[db] = mfma32(dsop[kc], qt, dk[db]);
-          }
+            for (int db = 0; db < 2; ++db) {
+              const bf16x8 dot = sw_tr_op(dos, 32 * qb + 16 * kc, 32 * db, lane);
+              const bf16x8 qt = sw_tr_op(qs, 32 * qb + 16 * kc, 32 * db, lane);
+              dv[db] = mfma32(pop[kc], dot, dv[db]);
+              dk[db] = mfma32(dsop[kc], qt, dk[db]);
+            }
+        }
         if (qb == 0) __builtin_amdgcn_sched_barrier(0);
       }
     }
