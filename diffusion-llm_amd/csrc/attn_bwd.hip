@@ -629,21 +629,26 @@ __device__ __forceinline__ void dq_item(const BwdArgs& a, __bf16* smem, int bh, 
     const int k0 = wave_uniform(tile_of(it) * kSwRows);
     const int c0 = bounds_class(cb, k0, 32, a.n);
     const int c1 = bounds_class(cb, k0 + 32, 32, a.n);
-    // One code path for every live tile (the accumulators keep their registers).
+    // One code path for every live tile (the accumulators keep their registers):
+    // its two 32-key blocks one after the other, each straight into dQ.
     if ((c0 | c1) != kNone) {
       const __bf16* ks = stage_k(cur);
       const __bf16* vs = stage_v(cur);
-      bf16x8 dsop[2][2];  // [key block][16-key step]
-      block_ops(ks, vs, k0, 0, c0 != kFull, dsop[0]);
-      block_ops(ks, vs, k0, 1, c1 != kFull, dsop[1]);
-      // dQ^T += K^T dS^T with K^T read transposed.
 #pragma unroll
-      for (int sb = 0; sb < 2; ++sb)
+      for (int sb = 0; sb < 2; ++sb) {
+        // MASK16: a block with no live pair for the wave's rows is skipped
+        // (the second block of a range's last tile for some waves).
+        if (!MASK16 || (sb ? c1 : c0) != kNone) {
+          bf16x8 dsop[2];  // [16-key step]
+          block_ops(ks, vs, k0, sb, (sb ? c1 : c0) != kFull, dsop);
+          // dQ^T += K^T dS^T with K^T read transposed.
 #pragma unroll
-        for (int kc = 0; kc < 2; ++kc)
+          for (int kc = 0; kc < 2; ++kc)
 #pragma unroll
-          for (int db = 0; db < 2; ++db)
-            dq[db] = mfma32(sw_tr_op(ks, 32 * sb + 16 * kc, 32 * db, lane), dsop[sb][kc], dq[db]);
+            for (int db = 0; db < 2; ++db)
+              dq[db] = mfma32(sw_tr_op(ks, 32 * sb + 16 * kc, 32 * db, lane), dsop[kc], dq[db]);
+        }
+      }
     }
     if (pf)
       vm_wait_barrier<4 * (kAhead - 1)>();

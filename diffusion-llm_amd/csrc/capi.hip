@@ -908,10 +908,16 @@ int bd3_train_tile_census(int32_t n, int32_t block_size, int64_t* out) {
   // The forward and the main launch's dQ items: with a block size dividing
   // 32 each noisy 32-row wave forms only its diagonal 32 x 32 block of its
   // one live diagonal key tile (a whole 32 x 64 tile in the count above).
-  const int64_t exec_dq = 32 % block_size == 0 ? exec_rows - (int64_t)(n / 32) * (32 * 64 - 32 * 32) : exec_rows;
+  const int64_t exec_fwd = 32 % block_size == 0 ? exec_rows - (int64_t)(n / 32) * (32 * 64 - 32 * 32) : exec_rows;
+  // With a block size a multiple of 16 both backward item kinds skip a 32 x
+  // 32 block with no live pair, so they compute every live 32 x 32 block
+  // once: 1024 pairs per full or partial sub-block counted above.
+  const bool blocks32 = block_size % 16 == 0;
+  const int64_t exec_dq = blocks32 ? 1024 * (full + partial) : exec_fwd;
+  if (blocks32) exec_keys = 1024 * (full + partial);
   const int64_t nn = n, bs = block_size;
   out[0] = useful;
-  out[1] = exec_dq;
+  out[1] = exec_fwd;
   out[2] = full;
   out[3] = partial;
   out[4] = skipped;

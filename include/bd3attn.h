@@ -428,10 +428,12 @@ int bd3_clock_probe(uint64_t* out, int32_t workgroups, int32_t iters, int64_t* w
  *      diagonal 32 x 32 block of the noisy keys),
  *    full / partial / skipped 32x32 sub-blocks of that schedule,
  *    useful pairs per (b,h) closed form n^2 + n*bs,
- *    pairs the main launch's dQ items compute (the forward's schedule),
+ *    pairs the main launch's dQ items compute (the forward's schedule; when
+ *      block_size % 16 == 0 every live 32 x 32 block once),
  *    pairs the dK/dV work computes (32-key waves, both 32-row halves of a
  *      64-row tile when either has a live pair; when 32 % block_size == 0
- *      only the diagonal 32 x 32 block of a noisy key tile's waves)}.
+ *      only the diagonal 32 x 32 block of a noisy key tile's waves; when
+ *      block_size % 16 == 0 every live 32 x 32 block once)}.
  * `out` must hold 8 values. Mirrors the reference's tile-skipping ranges
  * (kernels/BlockSparseFlashAttention.py:132-164, :274-325, :419-450) at the
  * library's own tile granularity.
