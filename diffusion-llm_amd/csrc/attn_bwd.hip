@@ -241,8 +241,8 @@ __device__ __forceinline__ void dkdv_item(const BwdArgs& a, __bf16* smem, int bh
   // 16-row x 1-key strips, so one test per lane for rows 0-15 of the block
   // (registers 0-7) and one for rows 16-31 decide it, and it enters the
   // exponent as an addend (0, or -inf for an invisible strip: exp2 gives 0);
-  // otherwise every pair is tested. A dead block is computed and fully
-  // masked.
+  // otherwise every pair is tested, and a dead block is computed and fully
+  // masked (with MASK16 the loop skips it).
   auto softmax_ops = [&](const f32x16& s, const f32x16& dp, int q0, int qb, bool masked, bf16x8 (&pop)[2],
                          bf16x8 (&dsop)[2]) {
     float blo = 0.f, bhi = 0.f;  // exponent addends of registers 0-7 and 8-15
@@ -580,8 +580,8 @@ __device__ __forceinline__ void dq_item(const BwdArgs& a, __bf16* smem, int bh, 
   // constant on 1-row x 16-key strips, so one test per lane for keys 0-15 of
   // the block (registers 0-7) and one for keys 16-31 decide it, and it
   // enters the exponent as its addend (-L, or -inf for an invisible strip);
-  // otherwise every pair is tested. A dead block is computed and fully
-  // masked.
+  // otherwise every pair is tested, and a dead block is computed and fully
+  // masked (with MASK16 the loop skips it).
   auto block_ops = [&](const __bf16* ks, const __bf16* vs, int k0, int sb, bool masked, bf16x8 (&dsop)[2]) {
     bf16x8 kop[4], vop[4];
 #pragma unroll

@@ -180,16 +180,16 @@ __device__ __forceinline__ void fwd_body(Args a) {
     vn.next(jumping);
   };
 
-  // The first two tiles are requested before waiting for Q, so the two
-  // latencies overlap. Consuming Q here (an empty asm reading it) makes the
-  // compiler place its own wait for the Q loads at this point; that wait
-  // also covers the direct loads issued after them, which is harmless.
   // Noisy rows with a block size dividing 32 (training, two-stage ring): the
   // walk's first two tiles are the workgroup's own noisy blocks, where each
   // wave's live pairs form the 32 x 32 block of its own rows (keys qrow0 ..
   // qrow0 + 31). Both tiles are loaded at once and every wave forms its block
   // in one half-tile step, instead of a whole-tile step on one of the two
   // tiles while the other two waves wait at its barrier.
+  // The first tiles are requested before waiting for Q, so the latencies
+  // overlap. Consuming Q here (an empty asm reading it) makes the compiler
+  // place its own wait for the Q loads at this point; that wait also covers
+  // the direct loads issued after them, which is harmless.
   bool diag_first = false;
   if constexpr (!PREFILL && kStages == 2) diag_first = q0 < a.n && 32 % a.bs == 0;
   if (diag_first) {
