@@ -20,7 +20,8 @@
 //   and dO rows live in registers as B operands; K, V key tiles come through
 //   LDS. S^T = K Q^T and dP^T = V dO^T put one row per lane, so L and Delta
 //   are per-lane scalars; dQ^T += K^T dS^T reads K^T from the LDS tile with
-//   ds_read_b64_tr_b16.
+//   ds_read_b64_tr_b16. The two 32-key blocks of a tile run one after the
+//   other, each straight into dQ.
 // dkdv_item (key-stationary): 4 waves of 32 keys. K and V rows live in
 //   registers as B operands of S = Q K^T and dP = dO V^T, which put one key
 //   per lane; query tiles (Q, dO, -L / scale, Delta) come through LDS.
@@ -28,6 +29,9 @@
 //   dO / Q transposed from LDS; the two 32-row blocks of a tile run one after
 //   the other, so three waves fit a SIMD next to the dQ items. dK, dV are
 //   written through LDS as 16-byte rows.
+// With a block size a multiple of 16 (MASK16) a partial block's mask is one
+//   test per 16-wide strip, entered as the exponent's addend (-inf for an
+//   invisible strip), and a block with no live pair for the wave is skipped.
 // Noisy key tiles with a block size dividing 32 (a noisy key is seen only by
 //   the noisy rows of its own block, so only the tile's diagonal 32 x 32
 //   blocks are live): in a launch with both kinds they get no dK/dV item;
@@ -39,7 +43,8 @@
 //   diagonal block.
 // Every score is the exact fp32 dot product of the bf16 rows; scale and
 // log2(e) are applied in fp32 (dQ: one FMA per element; dK/dV: the chain
-// starts from -L / scale and the result is multiplied by scale * log2(e)).
+// starts from -L / scale and the result is scaled by scale * log2(e) in the
+// exponent's FMA).
 // Both item kinds load their tiles global -> LDS with global_load_lds into
 // three-stage rings of swizzled tiles (bd3_swz.h), two tiles ahead, with one
 // counted vmcnt wait and barrier per tile, in one LDS buffer of the larger
