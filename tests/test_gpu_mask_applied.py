@@ -35,7 +35,7 @@ SCALE = 1.0 / D ** 0.5
 BUCKETS = {"mod64": lambda j: j % 64, "div64": lambda j: (j // 64) % 64}
 
 # (n, block size): MASK16 instances (bs % 16 == 0) and per-element ones.
-TRAIN = [(128, 1), (384, 3), (128, 4), (896, 7), (256, 16), (1024, 16), (2048, 16),
+TRAIN = [(128, 1), (384, 3), (128, 4), (384, 8), (896, 7), (256, 16), (256, 32), (1024, 16), (2048, 16),
          (256, 64), (512, 100), (512, 256), (2048, 256)]
 
 
